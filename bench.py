@@ -1,0 +1,224 @@
+"""Benchmark: full CausVid-shape history restore on one MI355X.
+
+A step restores the 7-chunk history (32,760 tokens) of all 30 layers, K and V,
+into bf16 [1, T, 12, 128] caches: per layer one ``reconstruct`` call of 14 jobs
+(uint8 codes [4680, r] with per-column affine, shared bf16 bases r_K = 128 /
+r_V = 192, Wan 3-D RoPE on K).  Inputs are synthetic, seeded and resident in HBM
+before timing.
+
+Printed JSON line (one): ``value`` = restored KV bytes written per second
+(GB/s, whole job), ``ms_per_step``, per-layer latency, the ``roofline`` of the
+fused restore kernel (algorithmic bytes per launch / its average duration,
+measured with HIP events on the launch stream) and a ``cpu_baseline`` (the
+oracle's CPU restatement on a bounded sample, timed on this host).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+LAYERS, HEADS, HEAD_DIM = 30, 12, 128
+GRID = (3, 30, 52)
+CHUNKS = 7
+RANK_K, RANK_V = 128, 192
+CHANNELS = HEADS * HEAD_DIM
+TOKENS = GRID[0] * GRID[1] * GRID[2]
+HISTORY = CHUNKS * TOKENS
+METRIC = "restored KV GB/s + per-layer restore latency (CausVid shape, 1 GPU); fit chunks/s"
+
+
+def layer_bytes():
+    """Algorithmic HBM bytes of one layer's restore: bf16 K and V written, uint8 codes,
+    bf16 bases and fp32 affine read."""
+    written = 2 * HISTORY * CHANNELS * 2
+    codes = CHUNKS * TOKENS * (RANK_K + RANK_V)
+    basis = (RANK_K + RANK_V) * CHANNELS * 2
+    affine = CHUNKS * (RANK_K + RANK_V) * 2 * 4
+    return written, written + codes + basis + affine
+
+
+def layer_flops():
+    return 2 * CHUNKS * TOKENS * CHANNELS * (RANK_K + RANK_V)
+
+
+def covering_affine(rank, rng):
+    lo = rng.uniform(-4, 0, size=rank).astype(np.float32)
+    hi = (lo.astype(np.float64) + rng.uniform(0.5, 6, size=rank)).astype(np.float32)
+    from reelcache_amd.quantize import covering_affine as cover
+
+    affine = cover(lo, hi)
+    return affine[0].copy(), affine[1].copy()
+
+
+def build_workload(device, seed=0):
+    from reelcache_amd import restore_kernels as rk
+
+    rng = np.random.default_rng(seed)
+    generator = torch.Generator(device=device).manual_seed(seed)
+    # Wan 3-D RoPE table (theta 10000, sections 22/21/21 pairs), float64 as the model builds it.
+    sixth = HEAD_DIM // 6
+    parts = []
+    for dim in (HEAD_DIM - 4 * sixth, 2 * sixth, 2 * sixth):
+        inverse = 1.0 / torch.pow(10000.0, torch.arange(0, dim, 2, dtype=torch.float64) / dim)
+        parts.append(torch.polar(torch.ones(64, dim // 2, dtype=torch.float64),
+                                 torch.outer(torch.arange(64, dtype=torch.float64), inverse)))
+    table = rk.RopeTable.from_complex(torch.cat(parts, dim=1))
+    table.kernel_tables(device)
+    layers = []
+    for layer in range(LAYERS):
+        cache_k = torch.empty((1, HISTORY, HEADS, HEAD_DIM), dtype=torch.bfloat16, device=device)
+        cache_v = torch.empty_like(cache_k)
+        basis_k = torch.linalg.qr(torch.randn(CHANNELS, RANK_K, device=device, generator=generator))[0].T
+        basis_v = torch.linalg.qr(torch.randn(CHANNELS, RANK_V, device=device, generator=generator))[0].T
+        basis_k = basis_k.contiguous().to(torch.bfloat16)
+        basis_v = basis_v.contiguous().to(torch.bfloat16)
+        jobs = []
+        for chunk in range(CHUNKS):
+            for cache, basis, rank, rope in ((cache_k, basis_k, RANK_K, True), (cache_v, basis_v, RANK_V, False)):
+                codes = torch.randint(0, 256, (TOKENS, rank), dtype=torch.uint8, device=device, generator=generator)
+                scale, offset = covering_affine(rank, rng)
+                jobs.append(rk.ReconstructionJob(
+                    rk.CoefficientSource(codes, scale, offset), rk.NativeView(cache, token_offset=chunk * TOKENS),
+                    GRID, basis, rank, rk.RopePositions(table, (GRID[0] * chunk, 0, 0)) if rope else None))
+        layers.append(jobs)
+    torch.cuda.synchronize(device)
+    return layers
+
+
+def restore_step(layers, stream, events=None):
+    from reelcache_amd import restore_kernels as rk
+
+    handles = []
+    for index, jobs in enumerate(layers):
+        stage = [] if events is not None else None
+        handles.append(rk.reconstruct(jobs, stream=stream, stage_events=stage))
+        if events is not None:
+            events.append(stage)
+    return handles
+
+
+def cpu_baseline(seconds_budget=20.0, seed=1):
+    """The oracle's CPU restatement of the reference restore (IEEE FP32 product, FP64 RoPE,
+    one bf16 cast) on a bounded sample: whole CausVid layers, as many as fit the budget."""
+    from oracle import restore as orc
+    from oracle.quantize import covering_affine as cover
+
+    rng = np.random.default_rng(seed)
+    threads = os.cpu_count() or 1
+    basis = {rank: np.linalg.qr(rng.standard_normal((CHANNELS, rank)))[0].T.astype(np.float32)
+             for rank in (RANK_K, RANK_V)}
+    cos, sin = np.real(orc.wan_freqs(HEAD_DIM, 64)), np.imag(orc.wan_freqs(HEAD_DIM, 64))
+    jobs = []
+    for chunk in range(CHUNKS):
+        for rank, rope in ((RANK_K, True), (RANK_V, False)):
+            codes = rng.integers(0, 256, size=(TOKENS, rank), dtype=np.uint8)
+            lo = rng.uniform(-4, 0, size=rank).astype(np.float32)
+            affine = cover(lo, (lo + rng.uniform(0.5, 6, size=rank)).astype(np.float32))
+            jobs.append((codes, affine, rank, orc.rope_cos_sin(cos, sin, orc.wan_sections(HEAD_DIM // 2),
+                                                               (GRID[0] * chunk, 0, 0), GRID) if rope else None))
+    written, _ = layer_bytes()
+    layers = 0
+    started = time.perf_counter()
+    while True:
+        for codes, affine, rank, rope in jobs:
+            coefficients = orc.dequantize(codes, affine[0], affine[1])
+            values = orc.reconstruct(coefficients, basis[rank], HEADS, rope, compute=np.float32)
+            orc.f32_to_bf16_bits(values.astype(np.float32))
+        layers += 1
+        elapsed = time.perf_counter() - started
+        if elapsed >= seconds_budget or layers >= 4:
+            break
+    return {"value": round(layers * written / elapsed / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{layers} CausVid layer(s) (7 chunks x K/V, 4680x1536, r 128/192) through oracle.restore "
+                      f"(numpy FP32 GEMM with BLAS threads, FP64 RoPE, bf16 cast) on {threads} host threads; "
+                      f"{elapsed:.1f} s, {elapsed / layers * 1e3:.0f} ms/layer"}
+
+
+def main():
+    parser = argparse.ArgumentParser(description=__doc__)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--cpu-seconds", type=float, default=20.0)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only; the restore shards by layer or head with no "
+                                   "exchange (see DESIGN.md), run with --gpus 1"}))
+        sys.exit(2)
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    layers = build_workload(device)
+    stream = torch.cuda.Stream(device)
+    with torch.cuda.stream(stream):
+        for _ in range(args.warmup):
+            for handle in restore_step(layers, stream):
+                handle.release()
+    torch.cuda.synchronize(device)
+
+    # Timed region: K full restores, kernel-stage events recorded on the launch stream.
+    stage_log = []
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(device)
+    begin = time.perf_counter()
+    start.record(stream)
+    handles = []
+    with torch.cuda.stream(stream):
+        for _ in range(args.steps):
+            handles.extend(restore_step(layers, stream, stage_log))
+    stop.record(stream)
+    torch.cuda.synchronize(device)
+    wall = time.perf_counter() - begin
+    for handle in handles:
+        handle.release()
+    gpu_ms = start.elapsed_time(stop)
+    ms_per_step = gpu_ms / args.steps
+    layer_ms = []
+    kernel_ms = []
+    for stage in stage_log:
+        marks = dict(stage)
+        layer_ms.append(marks["start"].elapsed_time(marks["fused"]))
+        kernel_ms.append(marks["pack"].elapsed_time(marks["fused"]))
+    written, algorithmic = layer_bytes()
+    value = LAYERS * written / (ms_per_step / 1e3) / 1e9
+    kernel_avg = float(np.mean(kernel_ms))
+    achieved = algorithmic / (kernel_avg / 1e3) / 1e9
+    result = {
+        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u8->fp16x2 MFMA->bf16", "data": "synthetic (seeded codes, orthonormal bases)",
+        "config": {"workload": "CausVid/Wan-1.3B-shape restore (BASELINE configs[1]): 30 layers x {K,V}, "
+                               "7 chunks x 4680 tokens, 12x128, r_K=128 r_V=192, bf16 basis, Wan 3-D RoPE",
+                   "precision": "fp16x2", "layers": LAYERS, "tokens": HISTORY, "channels": CHANNELS},
+        "per_layer_latency_us": round(float(np.mean(layer_ms)) * 1e3, 2),
+        "per_layer_latency_p50_us": round(float(np.median(layer_ms)) * 1e3, 2),
+        "restore_kernel_us": round(kernel_avg * 1e3, 2),
+        "wall_s": round(wall, 3),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "restore_kernel (fp16x2, u8 codes, KS=12)",
+                     "algorithmic_bytes_per_launch": algorithmic,
+                     "mfma_tflops": round(2 * layer_flops() / (kernel_avg / 1e3) / 1e12, 1)},
+        "fit_chunks_per_s": None,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

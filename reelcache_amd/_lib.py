@@ -1,0 +1,150 @@
+"""ctypes binding of ``libreelcache_hip.so`` (the C ABI declared in ``include/reelcache_hip.h``).
+
+The library is built ahead of time (``reelcache_amd.csrc.build``) and loaded on
+first use.  There is no fallback: when it is missing or was built for another
+ABI, every GPU entry point raises :class:`UnsupportedError` with the reason.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import numpy as np
+
+from .errors import ConfigurationError, UnsupportedError
+
+LIBRARY = Path(__file__).resolve().with_name("libreelcache_hip.so")
+ABI_VERSION = 1
+
+# Status codes (RCH_E_*).
+OK, E_CONFIG, E_UNSUPPORTED, E_LAUNCH = 0, 1, 2, 3
+
+# Precision codes follow the reference's PRECISIONS order (reelcache/restore_kernels.py:137).
+PRECISION_CODES = {"fp32": 0, "tf32": 1, "tf32x3": 2, "fp16": 3, "fp16x2": 4, "bf16": 5}
+DT_F32, DT_F16, DT_BF16, DT_U8, DT_F64 = 0, 1, 2, 3, 4
+SRC_FLOAT, SRC_U8, SRC_PICTURE, SRC_DENSE = 0, 1, 2, 3
+ROPE_NONE, ROPE_SEPARABLE, ROPE_DENSE = 0, 1, 2
+JF_SRC_VEC, JF_DST_VEC, JF_ROPE_VEC = 1, 2, 4
+
+# rch_job field order (40 x int64).
+JOB_FIELDS = (
+    "tokens", "rank", "frames", "grid_h", "grid_w",
+    "src_dtype", "src_ptr", "src_row_stride", "src_col_stride",
+    "scale_ptr", "offset_ptr", "coef_exp", "bound_ptr",
+    "pack_ptr", "pack_nblocks", "basis_exp_ptr",
+    "dst_ptr", "dst_token_stride", "dst_head_stride", "dst_dim_stride",
+    "rope", "cos_ptr", "sin_ptr", "rope_row_stride",
+    "row_t", "row_h", "row_w", "sec_t", "sec_h",
+    "pic_slots", "pic_planes", "pic_grid_cols", "pic_plane_stride", "pic_row_stride",
+    "pic_table_ptr", "flags", "reserved0", "reserved1", "reserved2", "reserved3",
+)
+JOB_DTYPE = np.dtype([(name, "<i8") for name in JOB_FIELDS])
+PACK_FIELDS = ("src_ptr", "src_dtype", "row_stride", "rank", "channels", "dst_ptr", "ksteps", "nblocks",
+               "amax_ptr", "exp_ptr", "reserved0", "reserved1")
+PACK_DTYPE = np.dtype([(name, "<i8") for name in PACK_FIELDS])
+
+_i, _i64, _p = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
+_SIGNATURES = {
+    "rch_abi_version": ([], _i),
+    "rch_job_size": ([], _i),
+    "rch_pack_size": ([], _i),
+    "rch_last_error": ([], ctypes.c_char_p),
+    "rch_fragment_bytes": ([_i], _i),
+    "rch_basis_absmax": ([_p, _i, _i64, _p], _i),
+    "rch_basis_pack": ([_p, _i, _i64, _i, _p], _i),
+    "rch_coefficient_bound": ([_p, _i, _p, _i, _i, _p], _i),
+    "rch_restore": ([_p, _i, _p, _i, _p, _i, _i, _i, _i, _i, _i, _i, _p], _i),
+    "rch_restore_occupancy": ([_i, _i, _i, ctypes.POINTER(_i)], _i),
+    "rch_rope_store": ([_p, _i, _p, _i, _i, _i, _i, _p], _i),
+}
+# Fit entry points are bound when present (declared in the same header).
+_OPTIONAL_SIGNATURES: dict = {}
+
+_LOCK = threading.Lock()
+_STATE: dict = {}
+
+
+def _load():
+    if not LIBRARY.exists():
+        raise UnsupportedError(
+            f"the HIP kernel library {LIBRARY.name} is not built; run reelcache_amd.csrc.build (hipcc, gfx950)")
+    try:
+        lib = ctypes.CDLL(str(LIBRARY))
+    except OSError as error:
+        raise UnsupportedError(f"the HIP kernel library could not be loaded: {error}") from error
+    for name, (arguments, result) in _SIGNATURES.items():
+        try:
+            function = getattr(lib, name)
+        except AttributeError as error:
+            raise UnsupportedError(f"{LIBRARY.name} does not export {name}; rebuild it") from error
+        function.argtypes, function.restype = arguments, result
+    for name, (arguments, result) in _OPTIONAL_SIGNATURES.items():
+        function = getattr(lib, name, None)
+        if function is not None:
+            function.argtypes, function.restype = arguments, result
+    if lib.rch_abi_version() != ABI_VERSION:
+        raise UnsupportedError(f"{LIBRARY.name} has ABI {lib.rch_abi_version()}, expected {ABI_VERSION}; rebuild it")
+    if lib.rch_job_size() != JOB_DTYPE.itemsize or lib.rch_pack_size() != PACK_DTYPE.itemsize:
+        raise UnsupportedError(f"{LIBRARY.name} descriptor layout differs from this package; rebuild it")
+    return lib
+
+
+def library():
+    """The loaded library (raises :class:`UnsupportedError` when unavailable)."""
+    with _LOCK:
+        if "lib" in _STATE:
+            return _STATE["lib"]
+        if "error" in _STATE:
+            raise UnsupportedError(_STATE["error"])
+        try:
+            _STATE["lib"] = _load()
+        except UnsupportedError as error:
+            _STATE["error"] = str(error)
+            raise
+        return _STATE["lib"]
+
+
+def unavailable_reason() -> str | None:
+    """Why the kernel library cannot be used in this process, or None."""
+    try:
+        library()
+    except UnsupportedError as error:
+        return str(error)
+    return None
+
+
+def register(signatures: dict) -> None:
+    """Declare further entry points (bound on first load, or now if already loaded)."""
+    _OPTIONAL_SIGNATURES.update(signatures)
+    lib = _STATE.get("lib")
+    if lib is not None:
+        for name, (arguments, result) in signatures.items():
+            function = getattr(lib, name, None)
+            if function is not None:
+                function.argtypes, function.restype = arguments, result
+
+
+def call(name: str, *arguments) -> None:
+    """Calls an entry point; maps a nonzero status to the declared error classes."""
+    lib = library()
+    function = getattr(lib, name, None)
+    if function is None:
+        raise UnsupportedError(f"{LIBRARY.name} does not export {name}; rebuild it")
+    status = function(*arguments)
+    if status == OK:
+        return
+    message = (lib.rch_last_error() or b"").decode(errors="replace")
+    if status == E_CONFIG:
+        raise ConfigurationError(message)
+    if status == E_UNSUPPORTED:
+        raise UnsupportedError(message)
+    raise RuntimeError(f"HIP launch failed: {message}")
+
+
+def occupancy(precision: int, source_kind: int, max_ksteps: int) -> int:
+    """Resident workgroups per CU of the restore variant for these arguments."""
+    blocks = ctypes.c_int(0)
+    call("rch_restore_occupancy", precision, source_kind, max_ksteps, ctypes.byref(blocks))
+    return blocks.value

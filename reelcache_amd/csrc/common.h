@@ -1,0 +1,47 @@
+// Shared helpers of the reelcache HIP library: status reporting and small device utilities.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/reelcache_hip.h"
+
+namespace rch {
+
+// Records `message` as this thread's last error and returns `code`.
+int fail(int code, const char* format, ...) __attribute__((format(printf, 2, 3)));
+
+// RCH_OK, or RCH_E_LAUNCH with the HIP error text when the last launch failed.
+int check_launch(const char* what);
+
+inline hipStream_t as_stream(void* stream) { return reinterpret_cast<hipStream_t>(stream); }
+
+// Workgroup index -> work unit, so that consecutive units land on the same XCD.
+// Workgroups are dispatched round-robin over the 8 XCDs of an MI355X (XCD = b % 8);
+// units [x*q + min(x, r), ...) run on XCD x.  A bijection on [0, G).
+__device__ __forceinline__ int xcd_unit(int b, int grid) {
+    constexpr int kXcds = 8;
+    const int q = grid / kXcds, r = grid - q * kXcds;
+    const int x = b % kXcds, i = b / kXcds;
+    return x * q + (x < r ? x : r) + i;
+}
+
+// Exact 2**e as float for e in [-126, 127].
+__device__ __forceinline__ float pow2f(int e) { return __int_as_float((e + 127) << 23); }
+
+// ceil(log2(v)) for a finite v > 0, exactly (frexp: v = m * 2**E, m in [0.5, 1)).
+__device__ __forceinline__ int ceil_log2(float v) {
+    int e;
+    const float m = frexpf(v, &e);
+    return m == 0.5f ? e - 1 : e;
+}
+
+// The reference's power-of-two prescale exponent: max|x| lands in (2**13, 2**14]
+// (reelcache/restore_kernels.py:1386-1398), clamped to [-100, 100].
+__device__ __forceinline__ int prescale_exponent(float bound) {
+    if (!(bound > 0.0f)) return 0;
+    int e = 14 - ceil_log2(bound);
+    return e < -100 ? -100 : (e > 100 ? 100 : e);
+}
+
+}  // namespace rch
