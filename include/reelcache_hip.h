@@ -76,10 +76,10 @@ typedef struct rch_job {
     int64_t src_row_stride, src_col_stride;
     int64_t scale_ptr, offset_ptr; /* fp32 [rank] affine (uint8 / picture sources) */
     int64_t coef_exp;        /* power-of-two prescale exponent of the coefficients (fp16 modes) */
-    int64_t bound_ptr;       /* device fp32 max|coef| (float sources without a host bound), or 0 */
+    int64_t bound_index;     /* scratch word holding the device fp32 max|coef| (float sources without a host bound), or -1 */
     int64_t pack_ptr;        /* packed basis fragments (rch_basis_pack output) */
     int64_t pack_nblocks;    /* 32-channel blocks in the packed basis (even) */
-    int64_t basis_exp_ptr;   /* device int32 basis prescale exponent written by rch_basis_pack */
+    int64_t basis_exp_index; /* first scratch word of the pack's per-block exponents (written by rch_basis_pack) */
     int64_t dst_ptr;         /* byte address of (batch, token_offset, head 0, dim 0) */
     int64_t dst_token_stride, dst_head_stride, dst_dim_stride;
     int64_t rope;            /* RCH_ROPE_* */
@@ -105,8 +105,8 @@ typedef struct rch_pack {
     int64_t dst_ptr;         /* packed fragments: ksteps * nblocks * 64 * frag bytes */
     int64_t ksteps;          /* ceil(rank / 16) */
     int64_t nblocks;         /* 2 * ceil(channels / 64) */
-    int64_t amax_ptr;        /* device fp32 max|Q[:rank]| (from rch_basis_absmax), or 0 */
-    int64_t exp_ptr;         /* device int32: prescale exponent written here */
+    int64_t reserved2;
+    int64_t exp_ptr;         /* device int32 [nblocks]: per 32-channel-block prescale exponents written here */
     int64_t reserved[2];
 } rch_pack;                  /* 12 x int64 = 96 bytes */
 
@@ -118,29 +118,24 @@ const char* rch_last_error(void);
 int rch_fragment_bytes(int precision);
 
 /*
- * max|Q[:rank]| per basis (fp32, nonnegative), accumulated with integer
- * atomics into packs[i].amax_ptr, which the caller zero-fills first.
- * Needed only when a bf16/fp32 basis is packed as fp16 (prescale choice).
- * Reference: the FP16 basis is required as is (restore_kernels.py:1881-1882);
- * this is the bf16-basis superset.
- */
-int rch_basis_absmax(const rch_pack* packs_dev, int n_packs, int64_t max_elements, void* stream);
-
-/*
  * Pack bases into fragments for `precision` (fp16 for fp16/fp16x2, bf16 for
- * bf16, fp32 for fp32) and write each pack's prescale exponent.  Replaces
- * the per-tile basis loads of _fused_restore_kernel
- * (reelcache/restore_kernels.py:1495-1496).
+ * bf16, fp32 for fp32) and write each 32-channel block's prescale exponent
+ * (non-zero only when a bf16/fp32 basis is packed as fp16: an exact power of
+ * two bringing the block's max|Q| into (2**13, 2**14]).  The reference requires
+ * the fp16 basis as is (reelcache/restore_kernels.py:1881-1882); a bf16 basis is
+ * this build's superset.  Replaces the per-tile basis loads of
+ * _fused_restore_kernel (reelcache/restore_kernels.py:1495-1496).
+ * max_nblocks = the largest nblocks over the packs.
  */
-int rch_basis_pack(const rch_pack* packs_dev, int n_packs, int64_t max_fragments, int precision, void* stream);
+int rch_basis_pack(const rch_pack* packs_dev, int n_packs, int64_t max_nblocks, int precision, void* stream);
 
 /*
  * max|coefficient| per job for float sources in fp16 modes, written as fp32
- * bits with integer atomics into jobs[i].bound_ptr (zero-filled by the caller).
- * Replaces _bound_kernel (reelcache/restore_kernels.py:1587-1606).
+ * bits with integer atomics into scratch[jobs[i].bound_index] (zero-filled by
+ * the caller).  Replaces _bound_kernel (reelcache/restore_kernels.py:1587-1606).
  */
 int rch_coefficient_bound(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev, int n_tiles,
-                          int max_rank, void* stream);
+                          int max_rank, int32_t* scratch_dev, void* stream);
 
 /*
  * The fused restore: gather / dequantize coefficients, rank-view product on
@@ -152,12 +147,14 @@ int rch_coefficient_bound(const rch_job* jobs_dev, int n_jobs, const int32_t* ti
  *              [bounds[w'], bounds[w' + 1]) (w' = XCD-swizzled index), where unit
  *              u = tile * ceil(channels / 32) + 32-channel block.
  * max_ksteps = max ceil(rank / 16) over the group selects the compiled variant.
+ * scratch_dev holds the basis exponents and device coefficient bounds the
+ * descriptors index (basis_exp_index, bound_index).
  * Replaces _fused_restore_kernel / _fused_group / _two_pass_group
  * (reelcache/restore_kernels.py:1447-1515, :2025-2121).
  */
 int rch_restore(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev, int n_tiles, const int32_t* bounds_dev,
                 int grid, int channels, int head_dim, int source_kind, int out_dtype, int precision, int max_ksteps,
-                void* stream);
+                const int32_t* scratch_dev, void* stream);
 
 /*
  * Resident workgroups per CU of the rch_restore variant for these arguments

@@ -32,8 +32,8 @@ JF_SRC_VEC, JF_DST_VEC, JF_ROPE_VEC = 1, 2, 4
 JOB_FIELDS = (
     "tokens", "rank", "frames", "grid_h", "grid_w",
     "src_dtype", "src_ptr", "src_row_stride", "src_col_stride",
-    "scale_ptr", "offset_ptr", "coef_exp", "bound_ptr",
-    "pack_ptr", "pack_nblocks", "basis_exp_ptr",
+    "scale_ptr", "offset_ptr", "coef_exp", "bound_index",
+    "pack_ptr", "pack_nblocks", "basis_exp_index",
     "dst_ptr", "dst_token_stride", "dst_head_stride", "dst_dim_stride",
     "rope", "cos_ptr", "sin_ptr", "rope_row_stride",
     "row_t", "row_h", "row_w", "sec_t", "sec_h",
@@ -42,7 +42,7 @@ JOB_FIELDS = (
 )
 JOB_DTYPE = np.dtype([(name, "<i8") for name in JOB_FIELDS])
 PACK_FIELDS = ("src_ptr", "src_dtype", "row_stride", "rank", "channels", "dst_ptr", "ksteps", "nblocks",
-               "amax_ptr", "exp_ptr", "reserved0", "reserved1")
+               "reserved2", "exp_ptr", "reserved0", "reserved1")
 PACK_DTYPE = np.dtype([(name, "<i8") for name in PACK_FIELDS])
 
 _i, _i64, _p = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
@@ -52,10 +52,9 @@ _SIGNATURES = {
     "rch_pack_size": ([], _i),
     "rch_last_error": ([], ctypes.c_char_p),
     "rch_fragment_bytes": ([_i], _i),
-    "rch_basis_absmax": ([_p, _i, _i64, _p], _i),
     "rch_basis_pack": ([_p, _i, _i64, _i, _p], _i),
-    "rch_coefficient_bound": ([_p, _i, _p, _i, _i, _p], _i),
-    "rch_restore": ([_p, _i, _p, _i, _p, _i, _i, _i, _i, _i, _i, _i, _p], _i),
+    "rch_coefficient_bound": ([_p, _i, _p, _i, _i, _p, _p], _i),
+    "rch_restore": ([_p, _i, _p, _i, _p, _i, _i, _i, _i, _i, _i, _i, _p, _p], _i),
     "rch_restore_occupancy": ([_i, _i, _i, ctypes.POINTER(_i)], _i),
     "rch_rope_store": ([_p, _i, _p, _i, _i, _i, _i, _p], _i),
 }

@@ -12,62 +12,57 @@ namespace {
 // Basis packing
 // ---------------------------------------------------------------------------------------------
 
-__global__ void __launch_bounds__(256) basis_absmax_kernel(const rch_pack* __restrict__ packs) {
-    const rch_pack& P = packs[blockIdx.y];
-    const int64_t rows = P.rank, cols = P.channels, total = rows * cols;
-    float m = 0.0f;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
-         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        const int64_t r = i / cols, c = i - r * cols;
-        m = fmaxf(m, fabsf(load_value(P.src_ptr, r * P.row_stride + c, static_cast<int>(P.src_dtype))));
-    }
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    __shared__ float partial[4];
-    if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = m;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        m = fmaxf(fmaxf(partial[0], partial[1]), fmaxf(partial[2], partial[3]));
-        atomicMax(reinterpret_cast<unsigned int*>(P.amax_ptr), __float_as_uint(m));
-    }
-}
-
+// One wave per (basis, 32-channel block): lane l holds channel block_channel(l % 32) and the
+// rank slots of half l / 32.  Pass 1 reduces max|Q| over the block (fp16 fragments of a
+// non-fp16 basis are prescaled by 2**e so that it lands in (2**13, 2**14]; one exponent per
+// block, written to exps[block]); pass 2 writes the fragments of every 16-row step.
 template <int PREC>
 __global__ void __launch_bounds__(256) basis_pack_kernel(const rch_pack* __restrict__ packs) {
     const rch_pack& P = packs[blockIdx.y];
-    const int64_t total = P.ksteps * P.nblocks * 64;
-    const int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    const int dtype = static_cast<int>(P.src_dtype);
-    // fp16 fragments of a non-fp16 basis are prescaled by 2**e so that max|Q| lands in (2**13, 2**14].
-    const bool scaled = (PREC == RCH_PREC_FP16 || PREC == RCH_PREC_FP16X2) && dtype != RCH_DT_F16;
-    const int e = scaled ? prescale_exponent(*gin<float>(P.amax_ptr)) : 0;
-    if (q == 0) *gout<int32_t>(P.exp_ptr) = e;
-    if (q >= total) return;
-    const float pre = pow2f(e);
-    const int lane = static_cast<int>(q & 63);
-    const int64_t rest = q >> 6;
-    const int64_t nb = rest % P.nblocks, s = rest / P.nblocks;
-    const int h = lane >> 5;
+    const int64_t nb = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (nb >= P.nblocks) return;  // whole wave
+    const int lane = threadIdx.x & 63, h = lane >> 5;
     const int64_t c = 32 * nb + block_channel(lane & 31);
-    float v[8];
+    const int dtype = static_cast<int>(P.src_dtype);
+    const bool scaled = (PREC == RCH_PREC_FP16 || PREC == RCH_PREC_FP16X2) && dtype != RCH_DT_F16;
+    int e = 0;
+    if (scaled) {
+        float m = 0.0f;
+        for (int64_t s = 0; s < P.ksteps; ++s) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int64_t k = 16 * s + k_slot<PREC>(h, j);
-        v[j] = (k < P.rank && c < P.channels) ? load_value(P.src_ptr, k * P.row_stride + c, dtype) : 0.0f;
+            for (int j = 0; j < 8; ++j) {
+                const int64_t k = 16 * s + k_slot<PREC>(h, j);
+                if (k < P.rank && c < P.channels) m = fmaxf(m, fabsf(load_value(P.src_ptr, k * P.row_stride + c, dtype)));
+            }
+        }
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        e = prescale_exponent(m);
     }
-    if constexpr (PREC == RCH_PREC_FP32) {
-        RCH_GLOBAL f4* dst = gout<f4>(P.dst_ptr) + 2 * q;
-        dst[0] = f4{v[0], v[1], v[2], v[3]};
-        dst[1] = f4{v[4], v[5], v[6], v[7]};
-    } else if constexpr (PREC == RCH_PREC_BF16) {
-        bf8 out;
+    if (lane == 0) gout<int32_t>(P.exp_ptr)[nb] = e;
+    const float pre = pow2f(e);
+    for (int64_t s = 0; s < P.ksteps; ++s) {
+        const int64_t q = (s * P.nblocks + nb) * 64 + lane;
+        float v[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) out[j] = static_cast<__bf16>(v[j]);
-        gout<bf8>(P.dst_ptr)[q] = out;
-    } else {
-        h8 out;
+        for (int j = 0; j < 8; ++j) {
+            const int64_t k = 16 * s + k_slot<PREC>(h, j);
+            v[j] = (k < P.rank && c < P.channels) ? load_value(P.src_ptr, k * P.row_stride + c, dtype) : 0.0f;
+        }
+        if constexpr (PREC == RCH_PREC_FP32) {
+            RCH_GLOBAL f4* dst = gout<f4>(P.dst_ptr) + 2 * q;
+            dst[0] = f4{v[0], v[1], v[2], v[3]};
+            dst[1] = f4{v[4], v[5], v[6], v[7]};
+        } else if constexpr (PREC == RCH_PREC_BF16) {
+            bf8 out;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) out[j] = static_cast<_Float16>(v[j] * pre);
-        gout<h8>(P.dst_ptr)[q] = out;
+            for (int j = 0; j < 8; ++j) out[j] = static_cast<__bf16>(v[j]);
+            gout<bf8>(P.dst_ptr)[q] = out;
+        } else {
+            h8 out;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) out[j] = static_cast<_Float16>(v[j] * pre);
+            gout<h8>(P.dst_ptr)[q] = out;
+        }
     }
 }
 
@@ -76,11 +71,12 @@ __global__ void __launch_bounds__(256) basis_pack_kernel(const rch_pack* __restr
 // ---------------------------------------------------------------------------------------------
 
 __global__ void __launch_bounds__(256) coefficient_bound_kernel(const rch_job* __restrict__ jobs,
-                                                                const int32_t* __restrict__ tiles, int k_tiles) {
+                                                                const int32_t* __restrict__ tiles, int k_tiles,
+                                                                int32_t* __restrict__ scratch) {
     const int tile = blockIdx.x / k_tiles, kt = blockIdx.x - tile * k_tiles;
     const rch_job* J = jobs + tiles[2 * tile];
     const int64_t t0 = tiles[2 * tile + 1];
-    if (!J->bound_ptr) return;
+    if (J->bound_index < 0) return;
     const int dtype = static_cast<int>(J->src_dtype);
     float m = 0.0f;
     // 128 tokens x 64 rank columns per block; thread = (token, 32 columns).
@@ -96,7 +92,7 @@ __global__ void __launch_bounds__(256) coefficient_bound_kernel(const rch_job* _
     __syncthreads();
     if (threadIdx.x == 0) {
         m = fmaxf(fmaxf(partial[0], partial[1]), fmaxf(partial[2], partial[3]));
-        atomicMax(reinterpret_cast<unsigned int*>(J->bound_ptr), __float_as_uint(m));  // vector atomic
+        atomicMax(reinterpret_cast<unsigned int*>(scratch + J->bound_index), __float_as_uint(m));  // vector atomic
     }
 }
 
@@ -142,21 +138,10 @@ extern "C" {
 
 int rch_fragment_bytes(int precision) { return precision == RCH_PREC_FP32 ? 32 : 16; }
 
-int rch_basis_absmax(const rch_pack* packs_dev, int n_packs, int64_t max_elements, void* stream) {
-    if (!packs_dev || n_packs <= 0 || n_packs > 65535 || max_elements <= 0)
-        return fail(RCH_E_CONFIG, "rch_basis_absmax: invalid arguments");
-    int64_t blocks = (max_elements + 256 * 16 - 1) / (256 * 16);
-    if (blocks > 1024) blocks = 1024;
-    hipLaunchKernelGGL(basis_absmax_kernel, dim3(static_cast<unsigned>(blocks), n_packs), dim3(256), 0, as_stream(stream),
-                       packs_dev);
-    return check_launch("rch_basis_absmax");
-}
-
-int rch_basis_pack(const rch_pack* packs_dev, int n_packs, int64_t max_fragments, int precision, void* stream) {
-    if (!packs_dev || n_packs <= 0 || n_packs > 65535 || max_fragments <= 0)
+int rch_basis_pack(const rch_pack* packs_dev, int n_packs, int64_t max_nblocks, int precision, void* stream) {
+    if (!packs_dev || n_packs <= 0 || n_packs > 65535 || max_nblocks <= 0 || max_nblocks > 0x7fffffff)
         return fail(RCH_E_CONFIG, "rch_basis_pack: invalid arguments");
-    const int64_t blocks = (max_fragments + 255) / 256;
-    if (blocks > 0x7fffffff) return fail(RCH_E_CONFIG, "rch_basis_pack: basis too large");
+    const int64_t blocks = (max_nblocks + 3) / 4;
     const dim3 grid(static_cast<unsigned>(blocks), n_packs);
     hipStream_t s = as_stream(stream);
     switch (precision) {
@@ -170,14 +155,14 @@ int rch_basis_pack(const rch_pack* packs_dev, int n_packs, int64_t max_fragments
 }
 
 int rch_coefficient_bound(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev, int n_tiles, int max_rank,
-                          void* stream) {
-    if (!jobs_dev || !tiles_dev || n_jobs <= 0 || n_tiles <= 0 || max_rank <= 0)
+                          int32_t* scratch_dev, void* stream) {
+    if (!jobs_dev || !tiles_dev || !scratch_dev || n_jobs <= 0 || n_tiles <= 0 || max_rank <= 0)
         return fail(RCH_E_CONFIG, "rch_coefficient_bound: invalid arguments");
     const int k_tiles = (max_rank + 63) / 64;
     const int64_t blocks = static_cast<int64_t>(n_tiles) * k_tiles;
     if (blocks > 0x7fffffff) return fail(RCH_E_CONFIG, "rch_coefficient_bound: grid too large");
     hipLaunchKernelGGL(coefficient_bound_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, as_stream(stream),
-                       jobs_dev, tiles_dev, k_tiles);
+                       jobs_dev, tiles_dev, k_tiles, scratch_dev);
     return check_launch("rch_coefficient_bound");
 }
 
@@ -209,8 +194,8 @@ int rch_restore_occupancy(int precision, int source_kind, int max_ksteps, int* b
 
 int rch_restore(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev, int n_tiles, const int32_t* bounds_dev,
                 int grid, int channels, int head_dim, int source_kind, int out_dtype, int precision, int max_ksteps,
-                void* stream) {
-    if (!jobs_dev || !tiles_dev || !bounds_dev || n_jobs <= 0 || n_tiles <= 0 || grid <= 0 || channels <= 0 ||
+                const int32_t* scratch_dev, void* stream) {
+    if (!jobs_dev || !tiles_dev || !bounds_dev || !scratch_dev || n_jobs <= 0 || n_tiles <= 0 || grid <= 0 || channels <= 0 ||
         head_dim <= 0 || head_dim % 2 || max_ksteps <= 0 ||
         static_cast<int64_t>(n_tiles) * ((channels + 31) / 32) > 0x7fffffff)
         return fail(RCH_E_CONFIG, "rch_restore: invalid launch arguments");
@@ -220,7 +205,7 @@ int rch_restore(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev, i
     if (status) return status;
     const int nk = variant.chunked ? (max_ksteps + variant.ks - 1) / variant.ks : 1;
     hipLaunchKernelGGL(variant.fn, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, as_stream(stream), jobs_dev,
-                       tiles_dev, bounds_dev, nk, channels, head_dim, out_dtype);
+                       tiles_dev, bounds_dev, scratch_dev, nk, channels, head_dim, out_dtype);
     return check_launch("rch_restore");
 }
 

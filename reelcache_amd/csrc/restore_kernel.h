@@ -265,10 +265,42 @@ __device__ __forceinline__ int64_t picture_offset(const rch_job* J, int k, const
            (static_cast<int64_t>(cell_row) * J->grid_h + c.y) * J->pic_row_stride + cell_col * J->grid_w + c.x;
 }
 
+// Loads the cos/sin of the 8 pairs of channels c0 .. c0 + 15 (token t) into registers; the
+// values are consumed by rotate16 after the step's products, so the loads overlap the MFMAs.
+struct RopeRegs {
+    f4 c0, c1, s0, s1;
+    bool vec;
+};
+__device__ __forceinline__ RopeRegs load_rope(const rch_job* J, int kind, int c0, int head_dim, int64_t t, int f,
+                                              int y, int x) {
+    RopeRegs r;
+    r.vec = false;
+    const int d0 = c0 % head_dim;
+    if ((J->flags & RCH_JF_ROPE_VEC) && d0 + 16 <= head_dim) {
+        const int j0 = d0 >> 1;
+        const int64_t s0 = J->sec_t, s1 = J->sec_t + J->sec_h;
+        const int first = j0 < s0 ? 0 : (j0 < s1 ? 1 : 2);
+        const int last = j0 + 7 < s0 ? 0 : (j0 + 7 < s1 ? 1 : 2);
+        if (kind == RCH_ROPE_DENSE || first == last) {
+            const int64_t row = rope_row(J, kind, j0, t, f, y, x);
+            const RCH_GLOBAL f4* cv = reinterpret_cast<const RCH_GLOBAL f4*>(gin<float>(J->cos_ptr) + row * J->rope_row_stride + j0);
+            const RCH_GLOBAL f4* sv = reinterpret_cast<const RCH_GLOBAL f4*>(gin<float>(J->sin_ptr) + row * J->rope_row_stride + j0);
+            r.c0 = cv[0];
+            r.c1 = cv[1];
+            r.s0 = sv[0];
+            r.s1 = sv[1];
+            r.vec = true;
+        }
+    }
+    return r;
+}
+
 // Persistent fused restore.  Work units are (tile, 32-channel block) pairs, tile-major;
 // workgroup w processes the contiguous unit range [bounds[w'], bounds[w' + 1]) where w'
 // is its XCD-swizzled index, so neighbouring ranges share an XCD's L2.  The host sizes
-// the grid to the resident capacity and balances the ranges by rank (cost).
+// the grid to the resident capacity, balances the ranges by rank (cost) and launches
+// jobs of one rank class (KS) together, so the product loop is a fixed KS steps (steps
+// beyond a job's rank read zero fragments).
 //
 // CHUNKED: the rank exceeds KS steps; each unit runs nk = ceil(max steps / KS) k chunks
 // and rebuilds the coefficient fragments per chunk (slower; ranks beyond the register
@@ -276,7 +308,8 @@ __device__ __forceinline__ int64_t picture_offset(const rch_job* J, int k, const
 template <int PREC, int SRC, int KS, bool CHUNKED>
 __global__ void __launch_bounds__(kThreads, 2)
 restore_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict__ tiles,
-               const int32_t* __restrict__ bounds, int nk, int channels, int head_dim, int out_dtype) {
+               const int32_t* __restrict__ bounds, const int32_t* __restrict__ scratch, int nk, int channels,
+               int head_dim, int out_dtype) {
     constexpr int kFrag = PREC == RCH_PREC_FP32 ? 2 : 1;  // u4 per lane fragment
     constexpr int kStepFrags = 64 * kFrag;               // one 16-rank step of one 32-channel block
     constexpr int kBuffer = KS * kStepFrags;
@@ -305,16 +338,19 @@ restore_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict__ til
         tile = unit / blocks_per_tile;
         block = unit - tile * blocks_per_tile;
     };
+    // Rank steps of (a job in) this k chunk, clamped to [0, KS].
+    auto chunk_steps = [&](const rch_job* job, int kc) {
+        return max(0, min(KS, static_cast<int>((job->rank + 15) >> 4) - kc * KS));
+    };
 
     u4 staged[kPerThread];
     auto fetch = [&](int st) {
         int tile, block, kc;
         locate(st, tile, block, kc);
-        const rch_job* J = jobs + tiles[2 * tile];
-        const int ks = static_cast<int>((J->rank + 15) >> 4);
-        const int count = max(0, min(KS, ks - kc * KS)) * kStepFrags;
-        const RCH_GLOBAL u4* pack = gin<u4>(J->pack_ptr);
-        const int64_t nblocks = J->pack_nblocks;
+        const rch_job* job = jobs + tiles[2 * tile];
+        const int count = chunk_steps(job, kc) * kStepFrags;
+        const RCH_GLOBAL u4* pack = gin<u4>(job->pack_ptr);
+        const int64_t nblocks = job->pack_nblocks;
 #pragma unroll
         for (int i = 0; i < kPerThread; ++i) {
             const int q = tid + i * kThreads;
@@ -324,22 +360,20 @@ restore_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict__ til
             }
         }
     };
+    // Steps beyond the job's rank are written as zeros, so the product loop always runs KS steps.
     auto commit = [&](int st, int buffer) {
         int tile, block, kc;
         locate(st, tile, block, kc);
-        const rch_job* J = jobs + tiles[2 * tile];
-        const int ks = static_cast<int>((J->rank + 15) >> 4);
-        const int count = max(0, min(KS, ks - kc * KS)) * kStepFrags;
+        const int count = chunk_steps(jobs + tiles[2 * tile], kc) * kStepFrags;
 #pragma unroll
         for (int i = 0; i < kPerThread; ++i) {
             const int q = tid + i * kThreads;
-            if (q < count) lds[buffer][q] = staged[i];
+            if (q < kBuffer) lds[buffer][q] = q < count ? staged[i] : u4{0u, 0u, 0u, 0u};
         }
     };
 
-    // Tile state (uniform J; per-lane token).
-    const rch_job* J = nullptr;
-    int t0 = 0, ksteps = 0;
+    // Per-lane state of the current tile.
+    int current = -1;
     int64_t t = 0;
     bool valid = false;
     Coords xy = {0, 0, 0};
@@ -347,46 +381,68 @@ restore_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict__ til
 
     // Stages the codes of rank columns [kc*kRanks, (kc+1)*kRanks) of the tile's 128 tokens
     // (zero beyond the rank or the job) and their affine into LDS.
-    auto stage = [&](int kc) {
+    auto stage = [&](const rch_job* J, int t0, int kc) {
         const int k_lo = kc * kRanks;
         const int rank = static_cast<int>(J->rank);
         const int64_t tokens = J->tokens;
         if constexpr (SRC == RCH_SRC_U8) {
             const int64_t rs = J->src_row_stride, cs = J->src_col_stride;
             const bool vec = (J->flags & RCH_JF_SRC_VEC) != 0;
-            constexpr int kGroups = kRanks / 16;
-            for (int q = tid; q < kTileTokens * kGroups; q += kThreads) {
-                const int token = q / kGroups, g = q - token * kGroups;
-                const int64_t tt = t0 + token;
-                const int k0 = k_lo + 16 * g;
-                u4 bytes = {0u, 0u, 0u, 0u};
-                if (tt < tokens && k0 < rank) {
-                    if (vec && k0 + 16 <= rank) {
-                        bytes = *gin<u4>(J->src_ptr + tt * rs + k0);
-                    } else {
-                        uint32_t w[4] = {0u, 0u, 0u, 0u};
+            constexpr int kGroups = kRanks / 16;                       // 16-byte groups per token row
+            constexpr int kIters = (kTileTokens * kGroups + kThreads - 1) / kThreads;
+            if (vec && k_lo + kRanks <= rank && t0 + kTileTokens <= tokens) {
+                // Full tile, aligned rows: every thread issues all its 16-byte loads before any
+                // LDS write, so their latencies overlap.
+                u4 bytes[kIters];
+#pragma unroll
+                for (int i = 0; i < kIters; ++i) {
+                    const int q = tid + i * kThreads;
+                    const int token = q / kGroups, g = q - token * kGroups;
+                    if (q < kTileTokens * kGroups) bytes[i] = *gin<u4>(J->src_ptr + (t0 + token) * rs + k_lo + 16 * g);
+                }
+#pragma unroll
+                for (int i = 0; i < kIters; ++i) {
+                    const int q = tid + i * kThreads;
+                    const int token = q / kGroups, g = q - token * kGroups;
+                    if (q < kTileTokens * kGroups) {
+                        u2* dst = reinterpret_cast<u2*>(codes + token * kPitch + 16 * g);
+                        dst[0] = u2{bytes[i][0], bytes[i][1]};
+                        dst[1] = u2{bytes[i][2], bytes[i][3]};
+                    }
+                }
+            } else {
+                for (int q = tid; q < kTileTokens * kGroups; q += kThreads) {
+                    const int token = q / kGroups, g = q - token * kGroups;
+                    const int64_t tt = t0 + token;
+                    const int k0 = k_lo + 16 * g;
+                    uint32_t w[4] = {0u, 0u, 0u, 0u};
+                    if (tt < tokens) {
                         for (int i = 0; i < 16 && k0 + i < rank; ++i)
                             w[i >> 2] |= static_cast<uint32_t>(gin<uint8_t>(J->src_ptr)[tt * rs + (k0 + i) * cs])
                                          << (8 * (i & 3));
-                        bytes = u4{w[0], w[1], w[2], w[3]};
                     }
+                    u2* dst = reinterpret_cast<u2*>(codes + token * kPitch + 16 * g);
+                    dst[0] = u2{w[0], w[1]};
+                    dst[1] = u2{w[2], w[3]};
                 }
-                u2* dst = reinterpret_cast<u2*>(codes + token * kPitch + 16 * g);
-                dst[0] = u2{bytes[0], bytes[1]};
-                dst[1] = u2{bytes[2], bytes[3]};
             }
-        } else {  // pictures: one thread per (token, half of the rank columns)
+        } else {  // pictures: one thread per (token, half of the rank columns), 16 gathers in flight
             const int token = tid >> 1, half = tid & 1;
             const int64_t tt = t0 + token;
             uint8_t* row = codes + token * kPitch;
-            if (tt < tokens) {
-                const Coords c = coords(J, static_cast<int>(tt));
-                for (int kl = half; kl < kRanks; kl += 2) {
+            const bool live = tt < tokens;
+            const Coords c = coords(J, live ? static_cast<int>(tt) : 0);
+            for (int base = half; base < kRanks; base += 32) {
+                uint8_t got[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int kl = base + 2 * i;
                     const int k = k_lo + kl;
-                    row[kl] = k < rank ? gin<uint8_t>(J->src_ptr)[picture_offset(J, k, c)] : 0;
+                    got[i] = (live && kl < kRanks && k < rank) ? gin<uint8_t>(J->src_ptr)[picture_offset(J, k, c)] : 0;
                 }
-            } else {
-                for (int kl = half; kl < kRanks; kl += 2) row[kl] = 0;
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    if (base + 2 * i < kRanks) row[base + 2 * i] = got[i];
             }
         }
         for (int i = tid; i < kRanks; i += kThreads) {
@@ -397,10 +453,10 @@ restore_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict__ til
     };
 
     CoefFrag<PREC> cf[KS];
-    auto build = [&](int kc) {
+    auto build = [&](const rch_job* J, int t0, int kc) {
         if constexpr (kStaged) {
             __syncthreads();  // earlier readers of codes / affine are done
-            stage(kc);
+            stage(J, t0, kc);
             __syncthreads();
             const uint8_t* row = codes + (wave * 32 + col) * kPitch;
 #pragma unroll
@@ -453,7 +509,6 @@ restore_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict__ til
     };
 
     f16v acc = {};
-    int current = -1;
     fetch(0);
     commit(0, 0);
     __syncthreads();
@@ -461,48 +516,68 @@ restore_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict__ til
         const int buffer = st & 1;
         int tile, block, kc;
         locate(st, tile, block, kc);
+        // The job is re-derived from the restrict descriptor table every step: its fields are
+        // then uniform scalar loads instead of per-lane vector loads.
+        const rch_job* J = jobs + tiles[2 * tile];
         if (st + 1 < steps) fetch(st + 1);
         if (CHUNKED || tile != current) {
             if (tile != current) {
-                J = jobs + tiles[2 * tile];
-                t0 = tiles[2 * tile + 1];
-                ksteps = static_cast<int>((J->rank + 15) >> 4);
-                t = t0 + wave * 32 + col;
+                t = tiles[2 * tile + 1] + wave * 32 + col;
                 valid = t < J->tokens;
                 xy = coords(J, valid ? static_cast<int>(t) : 0);
                 // Power-of-two prescale of the coefficients (fp16 modes).
                 int coef_exp = static_cast<int>(J->coef_exp);
-                if (kFp16 && J->bound_ptr) coef_exp = prescale_exponent(*gin<float>(J->bound_ptr));
+                if (kFp16 && J->bound_index >= 0) coef_exp = prescale_exponent(__int_as_float(scratch[J->bound_index]));
                 pre = kFp16 ? pow2f(coef_exp) : 1.0f;
+                // Undo the coefficient prescale (exact; the basis block exponent is undone per block
+                // in the epilogue as a second exact factor).
                 inv = kFp16 ? pow2f(-coef_exp) : 1.0f;
                 current = tile;
             }
-            build(kc);
+            build(J, tiles[2 * tile + 1], kc);
         }
-        if (kc == 0) acc = f16v{};
-        const int kin = min(KS, ksteps - kc * KS);
-#pragma unroll
-        for (int s = 0; s < KS; ++s)
-            if (s < kin) acc = mfma_step<PREC>(&lds[buffer][s * kStepFrags + lane * kFrag], cf[s], acc);
         const int c0 = block * 32 + 16 * h;
-        if ((!CHUNKED || kc == nk - 1) && valid && c0 < channels) {
-            // Undo both power-of-two prescales (each exact; the basis exponent comes from the packer).
-            const float inv_basis = pow2f(-*gin<int32_t>(J->basis_exp_ptr));
+        const int rope = static_cast<int>(J->rope);
+        const bool store = (!CHUNKED || kc == nk - 1) && valid && c0 < channels;
+        RopeRegs rr;
+        rr.vec = false;
+        if (store && rope != RCH_ROPE_NONE) rr = load_rope(J, rope, c0, head_dim, t, xy.f, xy.y, xy.x);
+        if (kc == 0) acc = f16v{};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) acc = mfma_step<PREC>(&lds[buffer][s * kStepFrags + lane * kFrag], cf[s], acc);
+        // Commit the next step's fragments before this step's stores: on gfx9 stores and loads
+        // share vmcnt and complete in order, so waiting for the fetched fragments after issuing
+        // the stores would also wait for the stores to reach memory.
+        if (st + 1 < steps) commit(st + 1, buffer ^ 1);
+        if (store) {
+            // Block exponent of the packed basis (per 32-channel block, written by the packer).
+            const int basis_exp = scratch[J->basis_exp_index + block];
             float v[16];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = (acc[i] * inv) * inv_basis;
-            const int rope = static_cast<int>(J->rope);
-            if (rope != RCH_ROPE_NONE) apply_rope(J, rope, v, c0, channels, head_dim, t, xy.f, xy.y, xy.x);
+            for (int i = 0; i < 16; ++i) v[i] = acc[i] * inv;
+            const float inv_block = pow2f(-basis_exp);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] *= inv_block;
+            if (rope != RCH_ROPE_NONE) {
+                if (rr.vec) {
+#pragma unroll
+                    for (int p = 0; p < 4; ++p) {
+                        rotate(v[2 * p], v[2 * p + 1], rr.c0[p], rr.s0[p]);
+                        rotate(v[8 + 2 * p], v[8 + 2 * p + 1], rr.c1[p], rr.s1[p]);
+                    }
+                } else {
+                    apply_rope(J, rope, v, c0, channels, head_dim, t, xy.f, xy.y, xy.x);
+                }
+            }
             store16(J, v, c0, channels, head_dim, t, out_dtype);
         }
-        if (st + 1 < steps) commit(st + 1, buffer ^ 1);
         __syncthreads();
     }
 }
 
 }  // namespace
 
-typedef void (*RestoreFn)(const rch_job*, const int32_t*, const int32_t*, int, int, int, int);
+typedef void (*RestoreFn)(const rch_job*, const int32_t*, const int32_t*, const int32_t*, int, int, int, int);
 
 // A compiled variant: kernel, its register-resident rank steps and whether it chunks the rank.
 struct RestoreVariant {

@@ -1109,17 +1109,6 @@ class _Arena:
         return host
 
 
-def _tiles(jobs):
-    """int32 ``[tiles, 2]``: (job, first token) of every 128-token tile."""
-    counts = np.array([(job.tokens + TILE_TOKENS - 1) // TILE_TOKENS for job in jobs], dtype=np.int64)
-    total = int(counts.sum())
-    first = np.repeat(np.cumsum(counts) - counts, counts)
-    tiles = np.empty((total, 2), dtype=np.int32)
-    tiles[:, 0] = np.repeat(np.arange(len(jobs), dtype=np.int32), counts)
-    tiles[:, 1] = (np.arange(total, dtype=np.int64) - first) * TILE_TOKENS
-    return tiles
-
-
 def _balanced_bounds(tile_costs, blocks_per_tile, grid):
     """int32 ``[grid + 1]`` boundaries splitting the (tile, 32-channel block) units into
     ``grid`` contiguous ranges of near-equal cost."""
@@ -1138,24 +1127,51 @@ def _config_value(config, name):
     return config.get(name, _DEFAULT_CONFIG[name])
 
 
-class _Group:
-    """Descriptors, packs and launches of one homogeneous launch group on the HIP backend."""
+def _tiles(job_indices, jobs):
+    """int32 ``[tiles, 2]``: (job index, first token) of every 128-token tile of the given jobs."""
+    counts = np.array([(jobs[i].tokens + TILE_TOKENS - 1) // TILE_TOKENS for i in job_indices], dtype=np.int64)
+    total = int(counts.sum())
+    first = np.repeat(np.cumsum(counts) - counts, counts)
+    tiles = np.empty((total, 2), dtype=np.int32)
+    tiles[:, 0] = np.repeat(np.asarray(job_indices, dtype=np.int32), counts)
+    tiles[:, 1] = (np.arange(total, dtype=np.int64) - first) * TILE_TOKENS
+    return tiles
+
+
+_JOB_INDEX = {name: index for index, name in enumerate(_lib.JOB_FIELDS)}
+_OCCUPANCY: dict = {}
+
+
+def _occupancy(code, kind, max_ksteps):
+    """Resident restore workgroups per CU for a variant (cached: a runtime query per variant)."""
+    key = (code, kind, max_ksteps)
+    if key not in _OCCUPANCY:
+        _OCCUPANCY[key] = _lib.occupancy(code, kind, max_ksteps)
+    return _OCCUPANCY[key]
+
+
+class _CallPlan:
+    """Descriptors, basis packs and launches of one :func:`reconstruct` call on the HIP backend.
+
+    One descriptor table and one pinned upload per call; one basis-maximum launch (non-fp16
+    bases in the fp16 modes) and one packing launch for every basis of the call; then one
+    fused restore launch per launch group (source kind, output dtype, head geometry and rank
+    class) and one RoPE-store launch per group of dense sources.
+    """
 
     def __init__(self, jobs, device, stream, precision, config, keepalive):
         self.jobs = jobs
         self.device = device
         self.stream = stream
-        self.kind, self.src_dtype = _source_kind(jobs[0])
         self.precision = precision
         self.code = _lib.PRECISION_CODES[precision]
-        self.out_dtype = jobs[0].destination.tensor.dtype
-        self.channels = jobs[0].channels
-        self.head_dim = jobs[0].destination.head_dim
         self.config = config
         self.keepalive = keepalive
+        self.grids = []
 
     # -- per-job descriptor fields ------------------------------------------------------------
-    def _destination(self, row, job):
+    @staticmethod
+    def _destination(row, job):
         view = job.destination
         address = _destination_address(view)
         strides = view.strides()
@@ -1188,72 +1204,41 @@ class _Group:
             row["flags"] |= _lib.JF_ROPE_VEC
 
     def run(self, stage_events=None):
-        if self.kind == _lib.SRC_DENSE:
-            return self._run_dense(stage_events)
-        return self._run_factorized(stage_events)
-
-    def _run_dense(self, stage_events):
-        jobs = self.jobs
-        desc = np.zeros(len(jobs), dtype=_lib.JOB_DTYPE)
-        tables: dict = {}
-        for index, job in enumerate(jobs):
-            row = desc[index]
-            values = job.source.values
-            row["tokens"] = job.tokens
-            row["frames"], row["grid_h"], row["grid_w"] = job.grid
-            row["src_dtype"] = _DTYPE_CODES[values.dtype]
-            row["src_ptr"] = values.data_ptr()
-            row["src_row_stride"], row["src_col_stride"] = values.stride()
-            self._destination(row, job)
-            self._rope(row, job, tables)
-        tiles = _tiles(jobs)
+        jobs, precision = self.jobs, self.precision
+        fragment = 32 if precision == "fp32" else 16
+        fp16_mode = precision in ("fp16", "fp16x2")
         arena = _Arena()
-        desc_offset = arena.add(desc)
-        tile_offset = arena.add(tiles)
-        with torch.cuda.stream(self.stream):
-            device_buffer = torch.empty(arena.size, dtype=torch.uint8, device=self.device)
-        host = arena.upload(device_buffer, self.stream)
-        self.keepalive.extend((host, device_buffer))
-        base = device_buffer.data_ptr()
-        if stage_events is not None:
-            stage_events.append(("start", _record(self.stream)))
-        _lib.call("rch_rope_store", base + desc_offset, len(jobs), base + tile_offset, len(tiles), self.channels,
-                  self.head_dim, _DTYPE_CODES[self.out_dtype], self.stream.cuda_stream)
-        if stage_events is not None:
-            stage_events.append(("rope_store", _record(self.stream)))
-        return 1
+        # Descriptor rows as dicts (cheap to fill), converted to the int64 table once.
+        rows = [{"flags": 0} for _ in jobs]
+        patches = []  # (job index, field, arena offset)
+        tables: dict = {}
 
-    def _run_factorized(self, stage_events):
-        jobs, channels = self.jobs, self.channels
-        fragment = 32 if self.code == _lib.PRECISION_CODES["fp32"] else 16
-        fp16_mode = self.precision in ("fp16", "fp16x2")
-        nblocks = 2 * ((channels + 63) // 64)
-        # One pack per distinct basis tensor view, covering the largest rank any job uses from it.
+        # Bases: one pack per distinct basis view, covering the largest rank any job uses from it.
         packs: dict = {}
         for job in jobs:
+            if job.basis is None:
+                continue
             basis = job.basis
             if basis.dtype not in BASIS_DTYPES or basis.stride(1) != 1:
                 raise ConfigurationError("GPU kernels need a float16 (or bfloat16) basis with unit column stride")
             key = (basis.data_ptr(), basis.stride(0), basis.shape[1], basis.dtype)
             packs[key] = max(packs.get(key, 0), job.rank)
         pack_keys = list(packs)
+        n_packs = len(pack_keys)
         pack_index = {key: index for index, key in enumerate(pack_keys)}
-        pack_bytes = [((rank + 15) // 16) * nblocks * 64 * fragment for rank in packs.values()]
+        nblocks = [2 * ((key[2] + 63) // 64) for key in pack_keys]
+        pack_bytes = [((packs[key] + 15) // 16) * blocks * 64 * fragment for key, blocks in zip(pack_keys, nblocks)]
         pack_offsets = np.concatenate(([0], np.cumsum([(size + 255) // 256 * 256 for size in pack_bytes])))
-        need_absmax = fp16_mode and any(key[3] != torch.float16 for key in pack_keys)
-        need_bounds = [fp16_mode and self.kind == _lib.SRC_FLOAT and job.source.bound is None for job in jobs]
-        # Device workspace: packs, then int32 exponents and zero-filled fp32 maxima / bounds.
-        scratch_words = len(pack_keys) * 2 + len(jobs)
+        # Device workspace: packed fragments; int32 scratch words: per-block basis exponents of every
+        # pack, then zero-filled fp32 device coefficient bounds (one per job).
+        exp_first = np.concatenate(([0], np.cumsum(nblocks))).astype(np.int64)
+        bound_first = int(exp_first[-1])
         with torch.cuda.stream(self.stream):
             workspace = torch.empty(int(pack_offsets[-1]) + 256, dtype=torch.uint8, device=self.device)
-            scratch = torch.zeros(scratch_words, dtype=torch.int32, device=self.device)
+            scratch = torch.zeros(bound_first + len(jobs), dtype=torch.int32, device=self.device)
         self.keepalive.extend((workspace, scratch))
         pack_base, scratch_base = workspace.data_ptr(), scratch.data_ptr()
-        exp_ptr = lambda index: scratch_base + 4 * index  # noqa: E731
-        amax_ptr = lambda index: scratch_base + 4 * (len(pack_keys) + index)  # noqa: E731
-        bound_ptr = lambda index: scratch_base + 4 * (2 * len(pack_keys) + index)  # noqa: E731
-
-        pack_desc = np.zeros(len(pack_keys), dtype=_lib.PACK_DTYPE)
+        pack_desc = np.zeros(n_packs, dtype=_lib.PACK_DTYPE)
         for index, key in enumerate(pack_keys):
             row = pack_desc[index]
             row["src_ptr"], row["row_stride"], row["channels"] = key[0], key[1], key[2]
@@ -1261,23 +1246,29 @@ class _Group:
             row["rank"] = packs[key]
             row["dst_ptr"] = pack_base + int(pack_offsets[index])
             row["ksteps"] = (packs[key] + 15) // 16
-            row["nblocks"] = nblocks
-            row["amax_ptr"] = amax_ptr(index)
-            row["exp_ptr"] = exp_ptr(index)
+            row["nblocks"] = nblocks[index]
+            row["exp_ptr"] = scratch_base + 4 * int(exp_first[index])
 
-        arena = _Arena()
-        desc = np.zeros(len(jobs), dtype=_lib.JOB_DTYPE)
-        patches = []  # (job index, field, arena offset)
-        tables: dict = {}
+        bound_jobs = []
         for index, job in enumerate(jobs):
-            row = desc[index]
+            row = rows[index]
             source = job.source
-            row["tokens"], row["rank"] = job.tokens, job.rank
+            row["tokens"] = job.tokens
             row["frames"], row["grid_h"], row["grid_w"] = job.grid
+            row["bound_index"] = -1
+            self._destination(row, job)
+            self._rope(row, job, tables)
+            if isinstance(source, DenseSource):
+                values = source.values
+                row["src_dtype"] = _DTYPE_CODES[values.dtype]
+                row["src_ptr"] = values.data_ptr()
+                row["src_row_stride"], row["src_col_stride"] = values.stride()
+                continue
+            row["rank"] = job.rank
             key = (job.basis.data_ptr(), job.basis.stride(0), job.basis.shape[1], job.basis.dtype)
             row["pack_ptr"] = int(pack_desc[pack_index[key]]["dst_ptr"])
-            row["pack_nblocks"] = nblocks
-            row["basis_exp_ptr"] = exp_ptr(pack_index[key])
+            row["pack_nblocks"] = nblocks[pack_index[key]]
+            row["basis_exp_index"] = int(exp_first[pack_index[key]])
             if isinstance(source, PictureSource):
                 layout = source.layout
                 pointers = [[picture.data_ptr() for picture in segment] for segment in source.pictures]
@@ -1298,44 +1289,64 @@ class _Group:
                 row["src_dtype"] = _DTYPE_CODES[values.dtype]
                 row["src_row_stride"], row["src_col_stride"] = values.stride()
                 if source.quantized:
-                    scale, offset = source.scale[:job.rank], source.offset[:job.rank]
-                    if (values.data_ptr() % 16 == 0 and values.stride(1) == 1 and values.stride(0) % 16 == 0):
+                    scale, offset = source.scale, source.offset
+                    if values.data_ptr() % 16 == 0 and values.stride(1) == 1 and values.stride(0) % 16 == 0:
                         row["flags"] |= _lib.JF_SRC_VEC
                 else:
                     scale = offset = None
             if scale is not None:
-                patches.append((index, "scale_ptr", arena.add(np.ascontiguousarray(scale[:job.rank]))))
-                patches.append((index, "offset_ptr", arena.add(np.ascontiguousarray(offset[:job.rank]))))
+                patches.append((index, "scale_ptr", arena.add(scale[:job.rank])))
+                patches.append((index, "offset_ptr", arena.add(offset[:job.rank])))
                 if fp16_mode:
                     row["coef_exp"] = _prescale_exponent(_coefficient_bound(scale[:job.rank], offset[:job.rank]))
             elif fp16_mode:
                 if source.bound is not None:
                     row["coef_exp"] = _prescale_exponent(source.bound)
                 else:
-                    row["bound_ptr"] = bound_ptr(index)
-            self._destination(row, job)
-            self._rope(row, job, tables)
+                    row["bound_index"] = bound_first + index
+                    bound_jobs.append(index)
 
-        tiles = _tiles(jobs)
-        blocks_per_tile = (channels + 31) // 32
-        max_ksteps = max((job.rank + 15) // 16 for job in jobs)
-        passes = 2 if self.precision == "fp16x2" else (4 if self.precision == "fp32" else 1)
+        # Launch groups and their balanced persistent grids.
+        groups: dict = {}
+        for index, job in enumerate(jobs):
+            groups.setdefault(_group_key(job, precision), []).append(index)
+        compute_units = _compute_units(self.device)
+        passes = 2 if precision == "fp16x2" else (4 if precision == "fp32" else 1)
         store_cost = float(_config_value(self.config, "store_cost"))
-        tile_costs = np.array([((jobs[j].rank + 15) // 16) * passes + store_cost for j in tiles[:, 0]])
-        per_cu = self.config.get("workgroups_per_cu") or _lib.occupancy(self.code, self.kind, max_ksteps)
-        units = len(tiles) * blocks_per_tile
-        grid = int(max(1, min(units, _compute_units(self.device) * max(1, per_cu))))
-        bounds = _balanced_bounds(tile_costs, blocks_per_tile, grid)
-
-        tile_offset = arena.add(tiles)
-        bounds_offset = arena.add(bounds)
-        packs_offset = arena.add(pack_desc)
+        launches_planned = []
+        for key, members in groups.items():
+            kind = key[0]
+            tiles = _tiles(members, jobs)
+            first = jobs[members[0]]
+            channels, head_dim = first.channels, first.destination.head_dim
+            out_dtype = _DTYPE_CODES[first.destination.tensor.dtype]
+            tile_offset = arena.add(tiles)
+            if kind == _lib.SRC_DENSE:
+                launches_planned.append(("dense", tile_offset, len(tiles), channels, head_dim, out_dtype))
+                continue
+            blocks_per_tile = (channels + 31) // 32
+            max_ksteps = max((jobs[i].rank + 15) // 16 for i in members)
+            steps = np.array([(jobs[i].rank + 15) // 16 for i in tiles[:, 0]], dtype=np.float64)
+            per_cu = self.config.get("workgroups_per_cu") or _occupancy(self.code, kind, max_ksteps)
+            grid = int(max(1, min(len(tiles) * blocks_per_tile, compute_units * max(1, per_cu))))
+            bounds = _balanced_bounds(steps * passes + store_cost, blocks_per_tile, grid)
+            launches_planned.append(("restore", tile_offset, len(tiles), arena.add(bounds), grid, channels, head_dim,
+                                     kind, out_dtype, max_ksteps))
+            self.grids.append(grid)
+        bound_tiles = _tiles(bound_jobs, jobs) if bound_jobs else None
+        bound_tile_offset = arena.add(bound_tiles) if bound_jobs else None
+        packs_offset = arena.add(pack_desc) if n_packs else None
+        desc = np.zeros((len(jobs), len(_lib.JOB_FIELDS)), dtype=np.int64)
         desc_offset = arena.reserve(desc.nbytes)
         with torch.cuda.stream(self.stream):
             device_buffer = torch.empty(arena.size, dtype=torch.uint8, device=self.device)
         base = device_buffer.data_ptr()
         for index, name, offset in patches:
-            desc[index][name] = base + offset
+            rows[index][name] = base + offset
+        for index, row in enumerate(rows):
+            line = desc[index]
+            for name, value in row.items():
+                line[_JOB_INDEX[name]] = value
         arena.put(desc_offset, desc)
         host = arena.upload(device_buffer, self.stream)
         self.keepalive.extend((host, device_buffer))
@@ -1344,26 +1355,28 @@ class _Group:
         launches = 0
         if stage_events is not None:
             stage_events.append(("start", _record(self.stream)))
-        max_fragments = max(pack_desc["ksteps"] * pack_desc["nblocks"] * 64)
-        if need_absmax:
-            _lib.call("rch_basis_absmax", base + packs_offset, len(pack_keys), int(max(pack_desc["rank"]) * channels),
-                      hip_stream)
+        if n_packs:
+            _lib.call("rch_basis_pack", base + packs_offset, n_packs, int(max(nblocks)), self.code, hip_stream)
             launches += 1
-        _lib.call("rch_basis_pack", base + packs_offset, len(pack_keys), int(max_fragments), self.code, hip_stream)
-        launches += 1
         if stage_events is not None:
             stage_events.append(("pack", _record(self.stream)))
-        if any(need_bounds):
-            _lib.call("rch_coefficient_bound", base + desc_offset, len(jobs), base + tile_offset, len(tiles),
-                      int(max(job.rank for job in jobs)), hip_stream)
+        if bound_jobs:
+            _lib.call("rch_coefficient_bound", base + desc_offset, len(jobs), base + bound_tile_offset,
+                      len(bound_tiles), int(max(jobs[i].rank for i in bound_jobs)), scratch_base, hip_stream)
             launches += 1
-        _lib.call("rch_restore", base + desc_offset, len(jobs), base + tile_offset, len(tiles), base + bounds_offset,
-                  grid, channels, self.head_dim, self.kind, _DTYPE_CODES[self.out_dtype], self.code, max_ksteps,
-                  hip_stream)
-        launches += 1
+        for plan in launches_planned:
+            if plan[0] == "dense":
+                _, tile_offset, n_tiles, channels, head_dim, out_dtype = plan
+                _lib.call("rch_rope_store", base + desc_offset, len(jobs), base + tile_offset, n_tiles, channels,
+                          head_dim, out_dtype, hip_stream)
+            else:
+                _, tile_offset, n_tiles, bounds_offset, grid, channels, head_dim, kind, out_dtype, max_ksteps = plan
+                _lib.call("rch_restore", base + desc_offset, len(jobs), base + tile_offset, n_tiles,
+                          base + bounds_offset, grid, channels, head_dim, kind, out_dtype, self.code, max_ksteps,
+                          scratch_base, hip_stream)
+            launches += 1
         if stage_events is not None:
             stage_events.append(("fused", _record(self.stream)))
-        self.grid = grid
         return launches
 
 
@@ -1373,9 +1386,23 @@ def _record(stream):
     return event
 
 
-def _group_key(job):
+def _rank_class(precision, job):
+    """The compiled variant's register-resident rank steps for this job (see ``pick_ks`` in
+    csrc/restore_kernel.h); jobs of one class share a launch, so the product loop is fixed."""
+    if job.rank is None:
+        return 0
+    steps = (job.rank + 15) // 16
+    classes = (4, 8) if precision == "fp32" else ((2, 4, 8, 12) if precision == "fp16x2" else (2, 4, 8, 12, 16))
+    for size in classes:
+        if steps <= size:
+            return size
+    return -1  # chunked
+
+
+def _group_key(job, precision=None):
     kind, dtype = _source_kind(job)
-    return (kind, dtype, job.destination.tensor.dtype, job.destination.head_dim, job.channels)
+    return (kind, dtype, job.destination.tensor.dtype, job.destination.head_dim, job.channels,
+            _rank_class(precision, job) if precision is not None else 0)
 
 
 def _resolve_backend(backend, cuda):
@@ -1419,16 +1446,9 @@ def _merged_config(config):
 
 
 def _run_hip(jobs, *, precision, config, stream, device, keepalive, stage_events):
-    groups: dict = {}
-    for job in jobs:
-        groups.setdefault(_group_key(job), []).append(job)
-    launches = 0
-    grids = []
-    for group in groups.values():
-        plan = _Group(group, device, stream, precision, config, keepalive)
-        launches += plan.run(stage_events)
-        grids.append(getattr(plan, "grid", None))
-    return launches, grids
+    plan = _CallPlan(list(jobs), device, stream, precision, config, keepalive)
+    launches = plan.run(stage_events)
+    return launches, plan.grids
 
 
 class _null:
