@@ -165,10 +165,12 @@ def main():
     torch.cuda.set_device(device)
     layers = build_workload(device)
     stream = torch.cuda.Stream(device)
+    variants = []
     with torch.cuda.stream(stream):
         for _ in range(args.warmup):
             for handle in restore_step(layers, stream):
                 handle.release()
+                variants = handle.stats["variants"]
     torch.cuda.synchronize(device)
 
     # Timed region: K full restores, kernel-stage events recorded on the launch stream.
@@ -213,7 +215,7 @@ def main():
         "host_us_per_layer_call": round(enqueued / (args.steps * LAYERS) * 1e6, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "restore_kernel (fp16x2, u8 codes, KS=12)",
+                     "kernel": "basis pack + restore launches per layer call: " + ", ".join(variants),
                      "algorithmic_bytes_per_launch": algorithmic,
                      "mfma_tflops": round(2 * layer_flops() / (kernel_avg / 1e3) / 1e12, 1)},
         "fit_chunks_per_s": None,

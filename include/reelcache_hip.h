@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-#define RCH_ABI_VERSION 1
+#define RCH_ABI_VERSION 2
 
 /* Status codes (mapped to reelcache errors by the host). */
 #define RCH_OK 0
@@ -60,6 +60,13 @@ extern "C" {
 #define RCH_JF_DST_VEC 2   /* destination: unit dim stride, 16-byte aligned base and token/head strides, head_dim % 16 == 0 */
 #define RCH_JF_ROPE_VEC 4  /* RoPE tables: 16-byte aligned, row stride % 4 == 0, head_dim % 16 == 0 */
 
+/* Launch-group flags (rch_restore group_flags). */
+#define RCH_GF_FAST 1      /* every job: uint8 codes with RCH_JF_SRC_VEC or pictures, RCH_JF_DST_VEC,
+                              dst_bytes < 2**31, no device coefficient bound (bound_index < 0), and,
+                              with RoPE, an interleaved pairs table under 2**31 bytes with an even row
+                              stride; the group: head_dim % 32 == 0, channels == heads * head_dim */
+#define RCH_GF_ROPE 2      /* with RCH_GF_FAST: every job of the group has RoPE (otherwise none has) */
+
 /*
  * One reconstruction job: one restored [N, C] matrix written into one native
  * cache slot.  Replaces one row of the reference's int64 descriptor table
@@ -88,7 +95,10 @@ typedef struct rch_job {
     int64_t pic_slots, pic_planes, pic_grid_cols, pic_plane_stride, pic_row_stride;
     int64_t pic_table_ptr;   /* device int64 [segments * frames] byte offsets from src_ptr */
     int64_t flags;           /* RCH_JF_* */
-    int64_t reserved[4];
+    int64_t pairs_ptr;       /* fp32 [rows, rope_row_stride, 2] interleaved (cos, sin), or 0 */
+    int64_t pairs_bytes;     /* size of the pairs table in bytes */
+    int64_t dst_bytes;       /* bytes from dst_ptr to one past the slot's last element */
+    int64_t reserved;
 } rch_job;                   /* 40 x int64 = 320 bytes */
 
 /*
@@ -125,9 +135,10 @@ int rch_fragment_bytes(int precision);
  * the fp16 basis as is (reelcache/restore_kernels.py:1881-1882); a bf16 basis is
  * this build's superset.  Replaces the per-tile basis loads of
  * _fused_restore_kernel (reelcache/restore_kernels.py:1495-1496).
- * max_nblocks = the largest nblocks over the packs.
+ * max_nblocks / max_ksteps = the largest nblocks / ksteps over the packs.
  */
-int rch_basis_pack(const rch_pack* packs_dev, int n_packs, int64_t max_nblocks, int precision, void* stream);
+int rch_basis_pack(const rch_pack* packs_dev, int n_packs, int64_t max_nblocks, int64_t max_ksteps, int precision,
+                   void* stream);
 
 /*
  * max|coefficient| per job for float sources in fp16 modes, written as fp32
@@ -146,7 +157,8 @@ int rch_coefficient_bound(const rch_job* jobs_dev, int n_jobs, const int32_t* ti
  *   bounds_dev int32 [grid + 1]: workgroup w processes work units
  *              [bounds[w'], bounds[w' + 1]) (w' = XCD-swizzled index), where unit
  *              u = tile * ceil(channels / 32) + 32-channel block.
- * max_ksteps = max ceil(rank / 16) over the group selects the compiled variant.
+ * max_ksteps = max ceil(rank / 16) over the group selects the compiled variant;
+ * group_flags (RCH_GF_*) selects the straight-line variant for groups that qualify.
  * scratch_dev holds the basis exponents and device coefficient bounds the
  * descriptors index (basis_exp_index, bound_index).
  * Replaces _fused_restore_kernel / _fused_group / _two_pass_group
@@ -154,14 +166,15 @@ int rch_coefficient_bound(const rch_job* jobs_dev, int n_jobs, const int32_t* ti
  */
 int rch_restore(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev, int n_tiles, const int32_t* bounds_dev,
                 int grid, int channels, int head_dim, int source_kind, int out_dtype, int precision, int max_ksteps,
-                const int32_t* scratch_dev, void* stream);
+                int group_flags, const int32_t* scratch_dev, void* stream);
 
 /*
  * Resident workgroups per CU of the rch_restore variant for these arguments
  * (sizes the persistent grid).  Replaces _channel_group's occupancy rule
  * (reelcache/restore_kernels.py:1979-1992).
  */
-int rch_restore_occupancy(int precision, int source_kind, int max_ksteps, int* blocks_per_cu);
+int rch_restore_occupancy(int precision, int source_kind, int max_ksteps, int head_dim, int out_dtype, int group_flags,
+                          int* blocks_per_cu);
 
 /*
  * Dense rows -> RoPE -> cast -> native store (DenseSource jobs).

@@ -16,7 +16,7 @@ import numpy as np
 from .errors import ConfigurationError, UnsupportedError
 
 LIBRARY = Path(__file__).resolve().with_name("libreelcache_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # Status codes (RCH_E_*).
 OK, E_CONFIG, E_UNSUPPORTED, E_LAUNCH = 0, 1, 2, 3
@@ -27,6 +27,7 @@ DT_F32, DT_F16, DT_BF16, DT_U8, DT_F64 = 0, 1, 2, 3, 4
 SRC_FLOAT, SRC_U8, SRC_PICTURE, SRC_DENSE = 0, 1, 2, 3
 ROPE_NONE, ROPE_SEPARABLE, ROPE_DENSE = 0, 1, 2
 JF_SRC_VEC, JF_DST_VEC, JF_ROPE_VEC = 1, 2, 4
+GF_FAST, GF_ROPE = 1, 2
 
 # rch_job field order (40 x int64).
 JOB_FIELDS = (
@@ -38,7 +39,7 @@ JOB_FIELDS = (
     "rope", "cos_ptr", "sin_ptr", "rope_row_stride",
     "row_t", "row_h", "row_w", "sec_t", "sec_h",
     "pic_slots", "pic_planes", "pic_grid_cols", "pic_plane_stride", "pic_row_stride",
-    "pic_table_ptr", "flags", "reserved0", "reserved1", "reserved2", "reserved3",
+    "pic_table_ptr", "flags", "pairs_ptr", "pairs_bytes", "dst_bytes", "reserved",
 )
 JOB_DTYPE = np.dtype([(name, "<i8") for name in JOB_FIELDS])
 PACK_FIELDS = ("src_ptr", "src_dtype", "row_stride", "rank", "channels", "dst_ptr", "ksteps", "nblocks",
@@ -52,10 +53,10 @@ _SIGNATURES = {
     "rch_pack_size": ([], _i),
     "rch_last_error": ([], ctypes.c_char_p),
     "rch_fragment_bytes": ([_i], _i),
-    "rch_basis_pack": ([_p, _i, _i64, _i, _p], _i),
+    "rch_basis_pack": ([_p, _i, _i64, _i64, _i, _p], _i),
     "rch_coefficient_bound": ([_p, _i, _p, _i, _i, _p, _p], _i),
-    "rch_restore": ([_p, _i, _p, _i, _p, _i, _i, _i, _i, _i, _i, _i, _p, _p], _i),
-    "rch_restore_occupancy": ([_i, _i, _i, ctypes.POINTER(_i)], _i),
+    "rch_restore": ([_p, _i, _p, _i, _p, _i, _i, _i, _i, _i, _i, _i, _i, _p, _p], _i),
+    "rch_restore_occupancy": ([_i, _i, _i, _i, _i, _i, ctypes.POINTER(_i)], _i),
     "rch_rope_store": ([_p, _i, _p, _i, _i, _i, _i, _p], _i),
 }
 # Fit entry points are bound when present (declared in the same header).
@@ -142,8 +143,10 @@ def call(name: str, *arguments) -> None:
     raise RuntimeError(f"HIP launch failed: {message}")
 
 
-def occupancy(precision: int, source_kind: int, max_ksteps: int) -> int:
+def occupancy(precision: int, source_kind: int, max_ksteps: int, head_dim: int, out_dtype: int,
+              group_flags: int) -> int:
     """Resident workgroups per CU of the restore variant for these arguments."""
     blocks = ctypes.c_int(0)
-    call("rch_restore_occupancy", precision, source_kind, max_ksteps, ctypes.byref(blocks))
+    call("rch_restore_occupancy", precision, source_kind, max_ksteps, head_dim, out_dtype, group_flags,
+         ctypes.byref(blocks))
     return blocks.value

@@ -3,7 +3,7 @@
 //
 // Reference: reelcache/restore_kernels.py (_bound_kernel :1588-1606, _rope_store_kernel
 // :1557-1585, _fused_group / _two_pass_group :2025-2121).
-#include "restore_kernel.h"
+#include "restore_fast.h"
 
 namespace rch {
 namespace {
@@ -12,57 +12,114 @@ namespace {
 // Basis packing
 // ---------------------------------------------------------------------------------------------
 
-// One wave per (basis, 32-channel block): lane l holds channel block_channel(l % 32) and the
-// rank slots of half l / 32.  Pass 1 reduces max|Q| over the block (fp16 fragments of a
-// non-fp16 basis are prescaled by 2**e so that it lands in (2**13, 2**14]; one exponent per
-// block, written to exps[block]); pass 2 writes the fragments of every 16-row step.
+// Eight consecutive channels c .. c + 7 of basis row r as floats (zero beyond the channels).
+// `vec`: 16-byte aligned rows of 16-bit values (one load), else element loads.
+__device__ __forceinline__ void basis_row8(const rch_pack& P, int dtype, bool vec, int64_t r, int64_t c, float (&v)[8]) {
+    const int64_t base = r * P.row_stride + c;
+    if (vec && c + 8 <= P.channels) {
+        const u4 raw = *reinterpret_cast<const RCH_GLOBAL u4*>(P.src_ptr + 2 * base);
+        if (dtype == RCH_DT_F16) {
+            const h8 x = __builtin_bit_cast(h8, raw);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = static_cast<float>(x[j]);
+        } else {
+            const bf8 x = __builtin_bit_cast(bf8, raw);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = static_cast<float>(x[j]);
+        }
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = c + j < P.channels ? load_value(P.src_ptr, base + j, dtype) : 0.0f;
+}
+
+// Packs rows Q[:rank] of each basis into MFMA A-operand fragments.  Workgroup (g, sp, p) owns
+// 32-channel blocks 2g, 2g + 1 and 16-row steps 2sp, 2sp + 1 of basis p.  Fragment (s, nb, lane)
+// holds Q[16 s + k_slot(h, j), 32 nb + block_channel(lane % 32)] for j = 0..7 (h = lane / 32).
+// Fp16 fragments of a non-fp16 basis are prescaled by 2**e per 32-channel block so that the
+// block's max|Q| lands in (2**13, 2**14] (exact powers of two; e is written to exps[nb] and
+// undone by the restore epilogue).  Every workgroup reduces the max of its blocks itself
+// (rows are re-read from L2), so one launch suffices.
 template <int PREC>
 __global__ void __launch_bounds__(256) basis_pack_kernel(const rch_pack* __restrict__ packs) {
-    const rch_pack& P = packs[blockIdx.y];
-    const int64_t nb = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    if (nb >= P.nblocks) return;  // whole wave
-    const int lane = threadIdx.x & 63, h = lane >> 5;
-    const int64_t c = 32 * nb + block_channel(lane & 31);
+    const rch_pack& P = packs[blockIdx.z];
+    const int64_t nb0 = 2 * static_cast<int64_t>(blockIdx.x);
+    const int64_t s0 = 2 * static_cast<int64_t>(blockIdx.y);
+    if (nb0 >= P.nblocks || s0 >= P.ksteps) return;  // whole workgroup
+    const int tid = threadIdx.x;
     const int dtype = static_cast<int>(P.src_dtype);
+    const bool vec = (dtype == RCH_DT_F16 || dtype == RCH_DT_BF16) && P.src_ptr % 16 == 0 && (P.row_stride * 2) % 16 == 0;
     const bool scaled = (PREC == RCH_PREC_FP16 || PREC == RCH_PREC_FP16X2) && dtype != RCH_DT_F16;
-    int e = 0;
+    const int64_t c_base = 32 * nb0;  // first of the 64 channels
+    // Thread layout for row loads: 32 rows x 8 chunks of 8 channels.
+    const int row_lane = tid >> 3, chunk = tid & 7;
+    __shared__ float tile[32][64 + 4];
+    __shared__ float block_max[4][2];
+    __shared__ int block_exp[2];
     if (scaled) {
         float m = 0.0f;
-        for (int64_t s = 0; s < P.ksteps; ++s) {
+        for (int64_t r = row_lane; r < P.rank; r += 32) {
+            float v[8];
+            basis_row8(P, dtype, vec, r, c_base + 8 * chunk, v);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int64_t k = 16 * s + k_slot<PREC>(h, j);
-                if (k < P.rank && c < P.channels) m = fmaxf(m, fabsf(load_value(P.src_ptr, k * P.row_stride + c, dtype)));
-            }
+            for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[j]));
         }
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-        e = prescale_exponent(m);
+        // Block of this thread: chunk / 4.  Reduce over chunk bits 0-1 and the 8 row lanes of the wave.
+        m = fmaxf(m, __shfl_xor(m, 1));
+        m = fmaxf(m, __shfl_xor(m, 2));
+        m = fmaxf(m, __shfl_xor(m, 8));
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+        if ((tid & 63) == 0) block_max[tid >> 6][0] = m;
+        if ((tid & 63) == 4) block_max[tid >> 6][1] = m;
+        __syncthreads();
+        if (tid < 2) {
+            const float b = fmaxf(fmaxf(block_max[0][tid], block_max[1][tid]), fmaxf(block_max[2][tid], block_max[3][tid]));
+            block_exp[tid] = prescale_exponent(b);
+        }
+    } else if (tid < 2) {
+        block_exp[tid] = 0;
     }
-    if (lane == 0) gout<int32_t>(P.exp_ptr)[nb] = e;
-    const float pre = pow2f(e);
-    for (int64_t s = 0; s < P.ksteps; ++s) {
-        const int64_t q = (s * P.nblocks + nb) * 64 + lane;
+    __syncthreads();
+    if (blockIdx.y == 0 && tid < 2 && nb0 + tid < P.nblocks) gout<int32_t>(P.exp_ptr)[nb0 + tid] = block_exp[tid];
+    // Stage rows 16 s0 .. 16 s0 + 31 (zero beyond the rank) of the 64 channels.
+    {
+        const int64_t r = 16 * s0 + row_lane;
         float v[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int64_t k = 16 * s + k_slot<PREC>(h, j);
-            v[j] = (k < P.rank && c < P.channels) ? load_value(P.src_ptr, k * P.row_stride + c, dtype) : 0.0f;
-        }
-        if constexpr (PREC == RCH_PREC_FP32) {
-            RCH_GLOBAL f4* dst = gout<f4>(P.dst_ptr) + 2 * q;
-            dst[0] = f4{v[0], v[1], v[2], v[3]};
-            dst[1] = f4{v[4], v[5], v[6], v[7]};
-        } else if constexpr (PREC == RCH_PREC_BF16) {
-            bf8 out;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) out[j] = static_cast<__bf16>(v[j]);
-            gout<bf8>(P.dst_ptr)[q] = out;
+        if (r < P.rank) {
+            basis_row8(P, dtype, vec, r, c_base + 8 * chunk, v);
         } else {
-            h8 out;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) out[j] = static_cast<_Float16>(v[j] * pre);
-            gout<h8>(P.dst_ptr)[q] = out;
+            for (int j = 0; j < 8; ++j) v[j] = 0.0f;
         }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) tile[row_lane][8 * chunk + j] = v[j];
+    }
+    __syncthreads();
+    // Thread -> fragment: step s0 + (tid / 128), block nb0 + (tid / 64) % 2, lane tid % 64.
+    const int sl = tid >> 7, b = (tid >> 6) & 1, lane = tid & 63, h = lane >> 5;
+    const int64_t s = s0 + sl, nb = nb0 + b;
+    if (s >= P.ksteps || nb >= P.nblocks) return;
+    const int col = 32 * b + block_channel(lane & 31);
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = tile[16 * sl + k_slot<PREC>(h, j)][col];
+    const int64_t q = (s * P.nblocks + nb) * 64 + lane;
+    if constexpr (PREC == RCH_PREC_FP32) {
+        RCH_GLOBAL f4* dst = gout<f4>(P.dst_ptr) + 2 * q;
+        dst[0] = f4{v[0], v[1], v[2], v[3]};
+        dst[1] = f4{v[4], v[5], v[6], v[7]};
+    } else if constexpr (PREC == RCH_PREC_BF16) {
+        bf8 out;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) out[j] = static_cast<__bf16>(v[j]);
+        gout<bf8>(P.dst_ptr)[q] = out;
+    } else {
+        const float pre = pow2f(block_exp[b]);
+        h8 out;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) out[j] = static_cast<_Float16>(v[j] * pre);
+        gout<h8>(P.dst_ptr)[q] = out;
     }
 }
 
@@ -138,11 +195,12 @@ extern "C" {
 
 int rch_fragment_bytes(int precision) { return precision == RCH_PREC_FP32 ? 32 : 16; }
 
-int rch_basis_pack(const rch_pack* packs_dev, int n_packs, int64_t max_nblocks, int precision, void* stream) {
-    if (!packs_dev || n_packs <= 0 || n_packs > 65535 || max_nblocks <= 0 || max_nblocks > 0x7fffffff)
+int rch_basis_pack(const rch_pack* packs_dev, int n_packs, int64_t max_nblocks, int64_t max_ksteps, int precision,
+                   void* stream) {
+    if (!packs_dev || n_packs <= 0 || n_packs > 65535 || max_nblocks <= 0 || max_nblocks > 0x7fffffff ||
+        max_ksteps <= 0 || max_ksteps > 2 * 65535)
         return fail(RCH_E_CONFIG, "rch_basis_pack: invalid arguments");
-    const int64_t blocks = (max_nblocks + 3) / 4;
-    const dim3 grid(static_cast<unsigned>(blocks), n_packs);
+    const dim3 grid(static_cast<unsigned>((max_nblocks + 1) / 2), static_cast<unsigned>((max_ksteps + 1) / 2), n_packs);
     hipStream_t s = as_stream(stream);
     switch (precision) {
         case RCH_PREC_FP32: hipLaunchKernelGGL(basis_pack_kernel<RCH_PREC_FP32>, grid, dim3(256), 0, s, packs_dev); break;
@@ -166,26 +224,55 @@ int rch_coefficient_bound(const rch_job* jobs_dev, int n_jobs, const int32_t* ti
     return check_launch("rch_coefficient_bound");
 }
 
-static int pick_variant(int precision, int source_kind, int max_ksteps, RestoreVariant* out) {
+// The kernel an rch_restore launch group runs: the straight-line variant (restore_fast.h) when
+// the group qualifies and one is compiled for its rank, else the general restore_kernel.
+struct Launch {
+    const void* fn;
+    bool fast;
+    int ks;
+    bool chunked;
+};
+
+static int pick_launch(int precision, int source_kind, int max_ksteps, int head_dim, int out_dtype, int group_flags,
+                       Launch* out) {
+    if ((group_flags & RCH_GF_FAST) && head_dim % 32 == 0 &&
+        (source_kind == RCH_SRC_U8 || source_kind == RCH_SRC_PICTURE)) {
+        const bool rope = (group_flags & RCH_GF_ROPE) != 0;
+        FastFn fn = nullptr;
+        int ks = 0;
+        switch (precision) {
+            case RCH_PREC_FP16: fn = pick_fast_fp16(max_ksteps, rope, out_dtype, &ks); break;
+            case RCH_PREC_FP16X2: fn = pick_fast_fp16x2(max_ksteps, rope, out_dtype, &ks); break;
+            case RCH_PREC_BF16: fn = pick_fast_bf16(max_ksteps, rope, out_dtype, &ks); break;
+            default: break;
+        }
+        if (fn) {
+            *out = {reinterpret_cast<const void*>(fn), true, ks, false};
+            return RCH_OK;
+        }
+    }
+    RestoreVariant variant;
     switch (precision) {
-        case RCH_PREC_FP32: *out = pick_restore_fp32(source_kind, max_ksteps); break;
-        case RCH_PREC_FP16: *out = pick_restore_fp16(source_kind, max_ksteps); break;
-        case RCH_PREC_FP16X2: *out = pick_restore_fp16x2(source_kind, max_ksteps); break;
-        case RCH_PREC_BF16: *out = pick_restore_bf16(source_kind, max_ksteps); break;
+        case RCH_PREC_FP32: variant = pick_restore_fp32(source_kind, max_ksteps); break;
+        case RCH_PREC_FP16: variant = pick_restore_fp16(source_kind, max_ksteps); break;
+        case RCH_PREC_FP16X2: variant = pick_restore_fp16x2(source_kind, max_ksteps); break;
+        case RCH_PREC_BF16: variant = pick_restore_bf16(source_kind, max_ksteps); break;
         default: return fail(RCH_E_UNSUPPORTED, "precision %d has no matrix-core path on gfx950", precision);
     }
-    if (!out->fn) return fail(RCH_E_CONFIG, "source kind %d is not a coefficient source", source_kind);
+    if (!variant.fn) return fail(RCH_E_CONFIG, "source kind %d is not a coefficient source", source_kind);
+    *out = {reinterpret_cast<const void*>(variant.fn), false, variant.ks, variant.chunked};
     return RCH_OK;
 }
 
-int rch_restore_occupancy(int precision, int source_kind, int max_ksteps, int* blocks_per_cu) {
-    if (!blocks_per_cu || max_ksteps <= 0) return fail(RCH_E_CONFIG, "rch_restore_occupancy: invalid arguments");
-    RestoreVariant variant;
-    const int status = pick_variant(precision, source_kind, max_ksteps, &variant);
+int rch_restore_occupancy(int precision, int source_kind, int max_ksteps, int head_dim, int out_dtype, int group_flags,
+                          int* blocks_per_cu) {
+    if (!blocks_per_cu || max_ksteps <= 0 || head_dim <= 0)
+        return fail(RCH_E_CONFIG, "rch_restore_occupancy: invalid arguments");
+    Launch launch;
+    const int status = pick_launch(precision, source_kind, max_ksteps, head_dim, out_dtype, group_flags, &launch);
     if (status) return status;
     int blocks = 0;
-    const hipError_t error = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &blocks, reinterpret_cast<const void*>(variant.fn), kThreads, 0);
+    const hipError_t error = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, launch.fn, kThreads, 0);
     if (error != hipSuccess)
         return fail(RCH_E_LAUNCH, "rch_restore_occupancy: %s", hipGetErrorString(error));
     *blocks_per_cu = blocks;
@@ -194,18 +281,27 @@ int rch_restore_occupancy(int precision, int source_kind, int max_ksteps, int* b
 
 int rch_restore(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev, int n_tiles, const int32_t* bounds_dev,
                 int grid, int channels, int head_dim, int source_kind, int out_dtype, int precision, int max_ksteps,
-                const int32_t* scratch_dev, void* stream) {
+                int group_flags, const int32_t* scratch_dev, void* stream) {
     if (!jobs_dev || !tiles_dev || !bounds_dev || !scratch_dev || n_jobs <= 0 || n_tiles <= 0 || grid <= 0 || channels <= 0 ||
         head_dim <= 0 || head_dim % 2 || max_ksteps <= 0 ||
         static_cast<int64_t>(n_tiles) * ((channels + 31) / 32) > 0x7fffffff)
         return fail(RCH_E_CONFIG, "rch_restore: invalid launch arguments");
     if (!valid_out(out_dtype)) return fail(RCH_E_CONFIG, "rch_restore: output dtype must be f32, f16 or bf16");
-    RestoreVariant variant;
-    const int status = pick_variant(precision, source_kind, max_ksteps, &variant);
+    if ((group_flags & RCH_GF_FAST) && channels % head_dim)
+        return fail(RCH_E_CONFIG, "rch_restore: RCH_GF_FAST needs channels == heads * head_dim");
+    Launch launch;
+    const int status = pick_launch(precision, source_kind, max_ksteps, head_dim, out_dtype, group_flags, &launch);
     if (status) return status;
-    const int nk = variant.chunked ? (max_ksteps + variant.ks - 1) / variant.ks : 1;
-    hipLaunchKernelGGL(variant.fn, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, as_stream(stream), jobs_dev,
-                       tiles_dev, bounds_dev, scratch_dev, nk, channels, head_dim, out_dtype);
+    if (launch.fast) {
+        hipLaunchKernelGGL(reinterpret_cast<FastFn>(const_cast<void*>(launch.fn)), dim3(static_cast<unsigned>(grid)),
+                           dim3(kThreads), 0, as_stream(stream), jobs_dev, tiles_dev, bounds_dev, scratch_dev,
+                           channels / head_dim, head_dim);
+    } else {
+        const int nk = launch.chunked ? (max_ksteps + launch.ks - 1) / launch.ks : 1;
+        hipLaunchKernelGGL(reinterpret_cast<RestoreFn>(const_cast<void*>(launch.fn)), dim3(static_cast<unsigned>(grid)),
+                           dim3(kThreads), 0, as_stream(stream), jobs_dev, tiles_dev, bounds_dev, scratch_dev, nk,
+                           channels, head_dim, out_dtype);
+    }
     return check_launch("rch_restore");
 }
 

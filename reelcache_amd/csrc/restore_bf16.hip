@@ -1,8 +1,12 @@
 // bf16 variants of the fused restore kernel (one translation unit per precision).
-#include "restore_kernel.h"
+#include "restore_fast.h"
 
 namespace rch {
 
 RestoreVariant pick_restore_bf16(int source_kind, int ks) { return pick_source<RCH_PREC_BF16>(source_kind, ks); }
+
+FastFn pick_fast_bf16(int ks, bool rope, int out_dtype, int* chosen) {
+    return pick_fast<RCH_PREC_BF16>(ks, rope, out_dtype, chosen);
+}
 
 }  // namespace rch

@@ -1,0 +1,354 @@
+#pragma once
+// Fast variant of the fused restore kernel (restore_kernel.h) for the common serving case:
+// fp16 / fp16x2 / bf16 products, uint8 (16-byte aligned rows) or picture codes, head_dim a
+// multiple of 32, destinations with unit dim stride and 16-byte aligned rows, slots and RoPE
+// tables under 2 GiB.  The host routes a launch group here only when every job qualifies
+// (RCH_GF_FAST); everything else runs restore_kernel.
+//
+// Same fragments, products and epilogue arithmetic as restore_kernel (identical bits); only
+// the schedule differs:
+//   * Every per-step memory access is a buffer instruction.  Lanes and steps that fall outside
+//     a job get an out-of-range offset (loads return zero, stores are dropped) instead of a
+//     branch, so a step is straight-line code with a fixed sequence of memory operations and
+//     the compiler waits for exactly the loads it needs.
+//   * gfx9 loads and stores share one in-order counter: waiting for a load also waits for
+//     every older store.  Basis fragments are fetched two steps ahead (register ring -> LDS
+//     buffer -> product) and RoPE values one step ahead, so no wait covers the stores of the
+//     step just finished.
+//   * Inside a tile the 32-channel blocks are walked position-major (dim block 0 of every
+//     head, then dim block 1, ...), so consecutive steps of a lane use the same RoPE rows.
+//   * Per-lane destination offsets and RoPE row offsets are computed once per tile; the
+//     (tile, dim block, head) cursor advances incrementally (no divisions per step).
+#include "restore_kernel.h"
+
+namespace rch {
+namespace {
+
+constexpr int kBufferWord3 = 0x00020000;  // raw buffer resource word 3 for the gfx9 family
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(int64_t base, int64_t bytes) {
+    const int records = bytes > 0x7fffffff ? 0x7fffffff : static_cast<int>(bytes < 0 ? 0 : bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(base), 0, records, kBufferWord3);
+}
+
+struct Cursor {
+    int tile, bp, head;
+};
+
+template <int PREC, int KS, bool ROPE, int OUT>
+__global__ void __launch_bounds__(kThreads, 2)
+restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict__ tiles,
+                    const int32_t* __restrict__ bounds, const int32_t* __restrict__ scratch, int heads,
+                    int head_dim) {
+    static_assert(PREC != RCH_PREC_FP32, "the fp32 mode runs restore_kernel");
+    constexpr int kStepFrags = 64;                       // u4 fragments of one 16-rank step of one block
+    constexpr int kBuffer = KS * kStepFrags;
+    constexpr int kPer = kBuffer / kThreads;
+    static_assert(kBuffer % kThreads == 0, "KS must be a multiple of 4: every thread moves whole fragments");
+    constexpr int kRanks = KS * 16;
+    constexpr int kPitch = kRanks + 8;
+    constexpr bool kFp16 = PREC == RCH_PREC_FP16 || PREC == RCH_PREC_FP16X2;
+    constexpr int kEsize = OUT == RCH_DT_F32 ? 4 : 2;
+    __shared__ u4 lds[2][kBuffer];
+    __shared__ __attribute__((aligned(16))) uint8_t codes[kTileTokens * kPitch];
+    __shared__ __attribute__((aligned(16))) float affine[2 * kRanks];
+
+    const int range = xcd_unit(blockIdx.x, gridDim.x);
+    const int first_unit = bounds[range];
+    const int steps = bounds[range + 1] - first_unit;
+    if (steps <= 0) return;
+    const int head_blocks = head_dim >> 5;
+    const int per_tile = heads * head_blocks;
+    const int last_tile = (first_unit + steps - 1) / per_tile;
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63, h = lane >> 5, col = lane & 31;
+
+    // Unit u of a tile is (dim block u / heads, head u % heads).  Prefetch cursors past the
+    // range end stay on the range's last tile (their fragments are fetched and never used).
+    auto advance = [&](Cursor c) __attribute__((always_inline)) {
+        c.head += 1;
+        const bool next_bp = c.head == heads;
+        c.head = next_bp ? 0 : c.head;
+        c.bp += next_bp ? 1 : 0;
+        const bool next_tile = c.bp == head_blocks;
+        c.bp = next_tile ? 0 : c.bp;
+        c.tile = min(c.tile + (next_tile ? 1 : 0), last_tile);
+        return c;
+    };
+
+    // Basis fragments of a step: thread loads fragments q = tid + i * 256 of the step's block
+    // (zero beyond the job's rank).
+    auto fetch = [&](const Cursor& c, u4 (&into)[kPer]) __attribute__((always_inline)) {
+        const rch_job* J = jobs + tiles[2 * c.tile];
+        const int ks = static_cast<int>((J->rank + 15) >> 4);
+        const int nblocks = static_cast<int>(J->pack_nblocks);
+        const __amdgpu_buffer_rsrc_t pack = make_rsrc(J->pack_ptr, int64_t(ks) * nblocks * 1024);
+        const uint32_t block_offset = static_cast<uint32_t>((c.head * head_blocks + c.bp) * 1024);
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int q = tid + i * kThreads;
+            const int s = q >> 6, li = q & 63;
+            const uint32_t offset = s < ks
+                                        ? static_cast<uint32_t>(s * nblocks) * 1024u + block_offset + li * 16
+                                        : kOutOfRange;
+            into[i] = __builtin_amdgcn_raw_buffer_load_b128(pack, offset, 0, 0);
+        }
+    };
+    auto commit = [&](int buffer, const u4 (&from)[kPer]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) lds[buffer][tid + i * kThreads] = from[i];
+    };
+
+    // Per-lane state of the current tile.
+    int current = -1;
+    uint32_t dst_lane = kOutOfRange;  // byte offset of this lane's 16 channels of (token, head 0, dim 0)
+    uint32_t row_t = 0, row_h = 0, row_w = 0;  // byte offsets of this token's RoPE rows
+    __amdgpu_buffer_rsrc_t dst = make_rsrc(0, 0), pairs = make_rsrc(0, 0);
+    int coef_exp = 0, sec0 = 0, sec1 = 0;
+    CoefFrag<PREC> cf[KS];
+
+    // Tile entry: stage the tile's codes and affine in LDS, convert this wave's 32 tokens to
+    // coefficient fragments.  All waves passed a barrier since they last read codes / affine.
+    auto enter = [&](const rch_job* J, int t0) __attribute__((always_inline)) {
+        const int64_t tokens = J->tokens;
+        const int64_t t = t0 + wave * 32 + col;
+        const bool valid = t < tokens;
+        const Coords xy = coords(J, valid ? static_cast<int>(t) : 0);
+        dst = make_rsrc(J->dst_ptr, J->dst_bytes);
+        dst_lane = valid ? static_cast<uint32_t>((t * J->dst_token_stride + 16 * h) * kEsize) : kOutOfRange;
+        if constexpr (ROPE) {
+            const int64_t row_bytes = J->rope_row_stride * 8;  // interleaved (cos, sin) fp32 pairs
+            pairs = make_rsrc(J->pairs_ptr, J->pairs_bytes);
+            // Dense tables: every pair uses row row_t + t.
+            const bool dense = J->rope == RCH_ROPE_DENSE;
+            const uint32_t first = static_cast<uint32_t>((J->row_t + (dense ? t : int64_t(xy.f))) * row_bytes);
+            const uint32_t second = static_cast<uint32_t>((J->row_h + xy.y) * row_bytes);
+            const uint32_t third = static_cast<uint32_t>((J->row_w + xy.x) * row_bytes);
+            row_t = first;
+            row_h = dense ? first : second;
+            row_w = dense ? first : third;
+            sec0 = static_cast<int>(J->sec_t);
+            sec1 = static_cast<int>(J->sec_t + J->sec_h);
+        }
+        coef_exp = kFp16 ? static_cast<int>(J->coef_exp) : 0;
+        const float pre = pow2f(coef_exp);
+        const int rank = static_cast<int>(J->rank);
+        if (J->pic_slots == 0) {  // uint8 rows, 16-byte aligned
+            const int64_t rs = J->src_row_stride;
+            constexpr int kGroups = kRanks / 16;
+            constexpr int kIters = (kTileTokens * kGroups + kThreads - 1) / kThreads;
+            const __amdgpu_buffer_rsrc_t src = make_rsrc(J->src_ptr + t0 * rs, (tokens - t0) * rs);
+            u4 bytes[kIters];
+#pragma unroll
+            for (int i = 0; i < kIters; ++i) {
+                const int q = tid + i * kThreads;
+                const int token = q / kGroups, g = q - token * kGroups;
+                const uint32_t offset = (q < kTileTokens * kGroups && 16 * g < rank)
+                                            ? static_cast<uint32_t>(token * rs + 16 * g)
+                                            : kOutOfRange;
+                bytes[i] = __builtin_amdgcn_raw_buffer_load_b128(src, offset, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < kIters; ++i) {
+                const int q = tid + i * kThreads;
+                const int token = q / kGroups, g = q - token * kGroups;
+                if (q < kTileTokens * kGroups) {
+                    u4 b = bytes[i];
+                    const int k0 = 16 * g;
+                    // Row padding beyond the rank reads as zero codes.
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) {
+                        const int keep = rank - (k0 + 4 * w);
+                        b[w] = keep >= 4 ? b[w] : (keep <= 0 ? 0u : (b[w] & ((1u << (8 * keep)) - 1u)));
+                    }
+                    u2* out = reinterpret_cast<u2*>(codes + token * kPitch + 16 * g);
+                    out[0] = u2{b[0], b[1]};
+                    out[1] = u2{b[2], b[3]};
+                }
+            }
+        } else {  // pictures: one thread per (token, half of the rank columns), 16 gathers in flight
+            const int token = tid >> 1, half = tid & 1;
+            const int64_t tt = t0 + token;
+            uint8_t* row = codes + token * kPitch;
+            const bool live = tt < tokens;
+            const Coords c = coords(J, live ? static_cast<int>(tt) : 0);
+            for (int base = half; base < kRanks; base += 32) {
+                uint8_t got[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int k = base + 2 * i;
+                    got[i] = (live && k < kRanks && k < rank) ? gin<uint8_t>(J->src_ptr)[picture_offset(J, k, c)] : 0;
+                }
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    if (base + 2 * i < kRanks) row[base + 2 * i] = got[i];
+            }
+        }
+        for (int i = tid; i < kRanks; i += kThreads) {
+            affine[i] = i < rank ? gin<float>(J->scale_ptr)[i] : 0.0f;
+            affine[kRanks + i] = i < rank ? gin<float>(J->offset_ptr)[i] : 0.0f;
+        }
+        __syncthreads();
+        const uint8_t* mine = codes + (wave * 32 + col) * kPitch;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const int kl = 16 * s + 8 * h;
+            const u2 b = *reinterpret_cast<const u2*>(mine + kl);
+            const f4 sc0 = *reinterpret_cast<const f4*>(affine + kl);
+            const f4 sc1 = *reinterpret_cast<const f4*>(affine + kl + 4);
+            const f4 of0 = *reinterpret_cast<const f4*>(affine + kRanks + kl);
+            const f4 of1 = *reinterpret_cast<const f4*>(affine + kRanks + kl + 4);
+            float a[8];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                a[j] = dequant((b[0] >> (8 * j)) & 0xffu, sc0[j], of0[j]);
+                a[j + 4] = dequant((b[1] >> (8 * j)) & 0xffu, sc1[j], of1[j]);
+            }
+            if (!valid) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) a[j] = 0.0f;
+            }
+            set_frag(cf[s], a, pre);
+        }
+    };
+
+    // (cos, sin) of this lane's 8 pairs j = 16 bp + 8 h + p of a dim block.  A pair's table row
+    // depends on its section: the section tests are uniform per lane half, so they reduce to
+    // scalar masks and one select per pair.
+    auto rope_load = [&](int bp, u2 (&into)[8]) __attribute__((always_inline)) {
+        const int jb = 16 * bp;
+        const uint32_t rt = row_t, rh = row_h, rw = row_w;  // values: a select of lvalues selects addresses
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+            const bool in_t = h ? (jb + 8 + p < sec0) : (jb + p < sec0);
+            const bool in_h = h ? (jb + 8 + p < sec1) : (jb + p < sec1);
+            const uint32_t row = in_t ? rt : (in_h ? rh : rw);
+            into[p] = __builtin_amdgcn_raw_buffer_load_b64(pairs, row + static_cast<uint32_t>((jb + 8 * h + p) * 8), 0, 0);
+        }
+    };
+
+    // One step: product of the staged block, scale, RoPE, cast, store.
+    auto finish = [&](const rch_job* J, const Cursor& c, int buffer, const u2 (&rope)[8]) __attribute__((always_inline)) {
+        f16v acc = {};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) acc = mfma_step<PREC>(&lds[buffer][s * kStepFrags + lane], cf[s], acc);
+        // Undo the coefficient prescale and the block's basis exponent (exact powers of two).
+        const int e = coef_exp + scratch[J->basis_exp_index + c.head * head_blocks + c.bp];
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = __builtin_amdgcn_ldexpf(acc[i], -e);
+        if constexpr (ROPE) {
+#pragma unroll
+            for (int p = 0; p < 8; ++p)
+                rotate(v[2 * p], v[2 * p + 1], __uint_as_float(rope[p][0]), __uint_as_float(rope[p][1]));
+        }
+        const uint32_t offset = dst_lane + static_cast<uint32_t>((c.head * J->dst_head_stride + c.bp * 32) * kEsize);
+        if constexpr (OUT == RCH_DT_F32) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const f4 out = {v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, out), dst, offset + 16 * q, 0, 0);
+            }
+        } else if constexpr (OUT == RCH_DT_BF16) {
+            bf8 a, b;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                a[i] = static_cast<__bf16>(v[i]);
+                b[i] = static_cast<__bf16>(v[i + 8]);
+            }
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, a), dst, offset, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, b), dst, offset + 16, 0, 0);
+        } else {
+            h8 a, b;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                a[i] = static_cast<_Float16>(v[i]);
+                b[i] = static_cast<_Float16>(v[i + 8]);
+            }
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, a), dst, offset, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, b), dst, offset + 16, 0, 0);
+        }
+    };
+
+    // Cursors of steps st (now), st + 1 and st + 2.
+    Cursor now;
+    {
+        now.tile = first_unit / per_tile;
+        const int local = first_unit - now.tile * per_tile;
+        now.bp = local / heads;
+        now.head = local - now.bp * heads;
+    }
+    Cursor ahead1 = advance(now), ahead2 = advance(ahead1);
+    u4 ring[kPer];
+    u2 rope_next[8], rope_now[8];
+
+    fetch(now, ring);
+    commit(0, ring);
+    fetch(ahead1, ring);
+    // Stores at out-of-range offsets (dropped by the hardware) after the prologue's ring loads.
+    // The wait the compiler places before the commit is shared by every step and must also hold
+    // for the path from this prologue; a step issues up to 12 memory operations after its ring
+    // loads (8 RoPE loads, 4 stores), so with at least as many here that wait covers just the
+    // ring loads instead of draining the stores of the previous step.
+#pragma unroll
+    for (int i = 0; i < 16; ++i) __builtin_amdgcn_raw_buffer_store_b32(0u, dst, kOutOfRange + 4 * i, 0, 0);
+    // Step st: the ring holds the fragments of step st + 1 (fetched during step st - 1); they go
+    // to the other LDS buffer, and the fragments of step st + 2 are fetched in their place.
+    // Each wait for the ring therefore covers loads issued a whole step earlier and none of the
+    // stores issued after them.
+    for (int st = 0; st < steps; ++st) {
+        const rch_job* J = jobs + tiles[2 * now.tile];
+        if (now.tile != current) {  // the first step enters its tile here too
+            enter(J, tiles[2 * now.tile + 1]);
+            current = now.tile;
+            if constexpr (ROPE) rope_load(now.bp, rope_now);
+        } else if constexpr (ROPE) {
+#pragma unroll
+            for (int p = 0; p < 8; ++p) rope_now[p] = rope_next[p];
+        }
+        commit((st + 1) & 1, ring);
+        fetch(ahead2, ring);
+        if constexpr (ROPE) rope_load(ahead1.bp, rope_next);
+        finish(J, now, st & 1, rope_now);
+        __syncthreads();
+        now = ahead1;
+        ahead1 = ahead2;
+        ahead2 = advance(ahead2);
+    }
+}
+
+typedef void (*FastFn)(const rch_job*, const int32_t*, const int32_t*, const int32_t*, int, int);
+
+template <int PREC, bool ROPE, int OUT>
+FastFn fast_ks(int ks, int* chosen) {
+    if (ks <= 4) { *chosen = 4; return restore_fast_kernel<PREC, 4, ROPE, OUT>; }
+    if (ks <= 8) { *chosen = 8; return restore_fast_kernel<PREC, 8, ROPE, OUT>; }
+    if (ks <= 12) { *chosen = 12; return restore_fast_kernel<PREC, 12, ROPE, OUT>; }
+    if constexpr (PREC != RCH_PREC_FP16X2) {
+        if (ks <= 16) { *chosen = 16; return restore_fast_kernel<PREC, 16, ROPE, OUT>; }
+    }
+    *chosen = 0;
+    return nullptr;
+}
+
+template <int PREC>
+FastFn pick_fast(int ks, bool rope, int out_dtype, int* chosen) {
+    switch (out_dtype) {
+        case RCH_DT_F32: return rope ? fast_ks<PREC, true, RCH_DT_F32>(ks, chosen) : fast_ks<PREC, false, RCH_DT_F32>(ks, chosen);
+        case RCH_DT_F16: return rope ? fast_ks<PREC, true, RCH_DT_F16>(ks, chosen) : fast_ks<PREC, false, RCH_DT_F16>(ks, chosen);
+        case RCH_DT_BF16: return rope ? fast_ks<PREC, true, RCH_DT_BF16>(ks, chosen) : fast_ks<PREC, false, RCH_DT_BF16>(ks, chosen);
+        default: *chosen = 0; return nullptr;
+    }
+}
+
+}  // namespace
+
+// One per precision translation unit (restore_<precision>.hip); nullptr when no fast variant
+// covers the rank.
+FastFn pick_fast_fp16(int ks, bool rope, int out_dtype, int* chosen);
+FastFn pick_fast_fp16x2(int ks, bool rope, int out_dtype, int* chosen);
+FastFn pick_fast_bf16(int ks, bool rope, int out_dtype, int* chosen);
+
+}  // namespace rch

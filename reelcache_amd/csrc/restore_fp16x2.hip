@@ -1,8 +1,12 @@
 // fp16x2 variants of the fused restore kernel (one translation unit per precision).
-#include "restore_kernel.h"
+#include "restore_fast.h"
 
 namespace rch {
 
 RestoreVariant pick_restore_fp16x2(int source_kind, int ks) { return pick_source<RCH_PREC_FP16X2>(source_kind, ks); }
+
+FastFn pick_fast_fp16x2(int ks, bool rope, int out_dtype, int* chosen) {
+    return pick_fast<RCH_PREC_FP16X2>(ks, rope, out_dtype, chosen);
+}
 
 }  // namespace rch

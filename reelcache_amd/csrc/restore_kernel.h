@@ -377,7 +377,8 @@ restore_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict__ til
     int64_t t = 0;
     bool valid = false;
     Coords xy = {0, 0, 0};
-    float pre = 1.0f, inv = 1.0f;
+    float pre = 1.0f;
+    int coef_exp = 0;
 
     // Stages the codes of rank columns [kc*kRanks, (kc+1)*kRanks) of the tile's 128 tokens
     // (zero beyond the rank or the job) and their affine into LDS.
@@ -525,13 +526,10 @@ restore_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict__ til
                 t = tiles[2 * tile + 1] + wave * 32 + col;
                 valid = t < J->tokens;
                 xy = coords(J, valid ? static_cast<int>(t) : 0);
-                // Power-of-two prescale of the coefficients (fp16 modes).
-                int coef_exp = static_cast<int>(J->coef_exp);
+                // Power-of-two prescale of the coefficients (fp16 modes), undone in the epilogue.
+                coef_exp = kFp16 ? static_cast<int>(J->coef_exp) : 0;
                 if (kFp16 && J->bound_index >= 0) coef_exp = prescale_exponent(__int_as_float(scratch[J->bound_index]));
-                pre = kFp16 ? pow2f(coef_exp) : 1.0f;
-                // Undo the coefficient prescale (exact; the basis block exponent is undone per block
-                // in the epilogue as a second exact factor).
-                inv = kFp16 ? pow2f(-coef_exp) : 1.0f;
+                pre = pow2f(coef_exp);
                 current = tile;
             }
             build(J, tiles[2 * tile + 1], kc);
@@ -550,14 +548,12 @@ restore_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict__ til
         // the stores would also wait for the stores to reach memory.
         if (st + 1 < steps) commit(st + 1, buffer ^ 1);
         if (store) {
-            // Block exponent of the packed basis (per 32-channel block, written by the packer).
-            const int basis_exp = scratch[J->basis_exp_index + block];
+            // Undo the coefficient prescale and the block exponent of the packed basis (per
+            // 32-channel block, written by the packer): one exact power-of-two scaling.
+            const int e = coef_exp + scratch[J->basis_exp_index + block];
             float v[16];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = acc[i] * inv;
-            const float inv_block = pow2f(-basis_exp);
-#pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] *= inv_block;
+            for (int i = 0; i < 16; ++i) v[i] = __builtin_amdgcn_ldexpf(acc[i], -e);
             if (rope != RCH_ROPE_NONE) {
                 if (rr.vec) {
 #pragma unroll

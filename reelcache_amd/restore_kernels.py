@@ -77,7 +77,7 @@ _DEFAULT_PRECISION = "fp16x2"
 _MATRIX_CORE_PRECISIONS = ("fp32", "fp16", "fp16x2", "bf16")
 TILE_TOKENS = 128  # tokens per workgroup tile (4 waves x 32)
 _DEFAULT_CONFIG = {"TILE_TOKENS": TILE_TOKENS, "BLOCK_N": 32, "waves": 4, "workgroups_per_cu": None,
-                   "store_cost": 4.0}
+                   "store_cost": 4.0, "fast_variant": True}
 # Triton tile keys the reference accepts in ``config``; they have no meaning for the HIP
 # kernels and are accepted (and ignored) so that caller configurations keep working.
 _REFERENCE_TILE_KEYS = {"BLOCK_M", "BLOCK_K", "num_warps", "num_stages", "N_GROUP", "PIC_T", "UNPACK_BLOCK_K",
@@ -240,10 +240,11 @@ def _upload_stream(device):
 class _KernelTables:
     """Contiguous FP32 device copies of one table and the event that completes them."""
 
-    __slots__ = ("cos", "event", "sin", "staging", "stamp")
+    __slots__ = ("cos", "event", "pairs", "sin", "staging", "stamp")
 
     def __init__(self, cos, sin, stamp, event=None, staging=None):
         self.cos, self.sin, self.stamp, self.event, self.staging = cos, sin, stamp, event, staging
+        self.pairs = None
 
     @classmethod
     def make(cls, cos, sin, device, stream, stamp):
@@ -424,6 +425,18 @@ class RopeTable:
         if entry.event is not None:
             entry.order_before(device, stream)
         return entry.cos, entry.sin
+
+    def kernel_pairs(self, device, stream=None):
+        """Interleaved float32 ``[rows, pairs, 2]`` (cos, sin) on ``device`` (built once per table
+        version, on ``stream``, from :meth:`kernel_tables`)."""
+        cos, sin = self.kernel_tables(device, stream)
+        entry = self._device_cache[cos.device]
+        if entry.pairs is None:
+            with torch.inference_mode(False), torch.no_grad():
+                stream = torch.cuda.current_stream(cos.device) if stream is None else stream
+                with torch.cuda.stream(stream):
+                    entry.pairs = torch.stack((cos, sin), dim=-1).contiguous()
+        return entry.pairs
 
 
 @dataclass(frozen=True, eq=False)
@@ -1142,12 +1155,33 @@ _JOB_INDEX = {name: index for index, name in enumerate(_lib.JOB_FIELDS)}
 _OCCUPANCY: dict = {}
 
 
-def _occupancy(code, kind, max_ksteps):
+def _occupancy(code, kind, max_ksteps, head_dim, out_dtype, group_flags):
     """Resident restore workgroups per CU for a variant (cached: a runtime query per variant)."""
-    key = (code, kind, max_ksteps)
+    key = (code, kind, max_ksteps, head_dim % 32 == 0, out_dtype, group_flags)
     if key not in _OCCUPANCY:
-        _OCCUPANCY[key] = _lib.occupancy(code, kind, max_ksteps)
+        _OCCUPANCY[key] = _lib.occupancy(code, kind, max_ksteps, head_dim, out_dtype, group_flags)
     return _OCCUPANCY[key]
+
+
+_FAST_LIMIT = 2 ** 31
+
+
+def _fast_flags(row, job, precision):
+    """``RCH_GF_*`` of one job: whether it qualifies for the straight-line restore kernel
+    (csrc/restore_fast.h), and whether it rotates."""
+    kind, _ = _source_kind(job)
+    flags = row["flags"]
+    if precision == "fp32" or job.destination.head_dim % 32 or row.get("bound_index", -1) >= 0:
+        return 0
+    if not (kind == _lib.SRC_PICTURE or (kind == _lib.SRC_U8 and flags & _lib.JF_SRC_VEC)):
+        return 0
+    if not flags & _lib.JF_DST_VEC or row["dst_bytes"] >= _FAST_LIMIT:
+        return 0
+    if job.rope is None:
+        return _lib.GF_FAST
+    if not row.get("pairs_ptr") or row["pairs_bytes"] >= _FAST_LIMIT:
+        return 0
+    return _lib.GF_FAST | _lib.GF_ROPE
 
 
 class _CallPlan:
@@ -1168,6 +1202,7 @@ class _CallPlan:
         self.config = config
         self.keepalive = keepalive
         self.grids = []
+        self.variants = []  # per restore launch: "fast" (straight-line kernel) or "general"
 
     # -- per-job descriptor fields ------------------------------------------------------------
     @staticmethod
@@ -1177,7 +1212,10 @@ class _CallPlan:
         strides = view.strides()
         row["dst_ptr"] = address
         row["dst_token_stride"], row["dst_head_stride"], row["dst_dim_stride"] = strides
-        per16 = 16 // view.tensor.element_size()
+        size = view.tensor.element_size()
+        row["dst_bytes"] = ((job.tokens - 1) * strides[0] + (view.heads - 1) * strides[1]
+                            + (view.head_dim - 1) * strides[2] + 1) * size
+        per16 = 16 // size
         if (address % 16 == 0 and strides[2] == 1 and strides[0] % per16 == 0 and strides[1] % per16 == 0
                 and view.head_dim % 16 == 0):
             row["flags"] |= _lib.JF_DST_VEC
@@ -1202,6 +1240,13 @@ class _CallPlan:
         if (cos.data_ptr() % 16 == 0 and sin.data_ptr() % 16 == 0 and cos.stride(0) % 4 == 0 and cos.stride(1) == 1
                 and sin.stride(0) == cos.stride(0) and job.destination.head_dim % 16 == 0):
             row["flags"] |= _lib.JF_ROPE_VEC
+        if job.destination.head_dim % 32 == 0 and cos.stride(0) % 2 == 0 and cos.stride(1) == 1:
+            pairs = tables.get(("pairs", id(table)))
+            if pairs is None:
+                pairs = table.kernel_pairs(self.device, self.stream)
+                tables[("pairs", id(table))] = pairs
+                self.keepalive.append(pairs)
+            row["pairs_ptr"], row["pairs_bytes"] = pairs.data_ptr(), pairs.numel() * 4
 
     def run(self, stage_events=None):
         jobs, precision = self.jobs, self.precision
@@ -1306,16 +1351,19 @@ class _CallPlan:
                     row["bound_index"] = bound_first + index
                     bound_jobs.append(index)
 
-        # Launch groups and their balanced persistent grids.
+        # Launch groups and their balanced persistent grids.  Jobs that qualify for the
+        # straight-line kernel (RCH_GF_FAST) are grouped apart, split by RoPE presence.
         groups: dict = {}
+        allow_fast = bool(_config_value(self.config, "fast_variant"))
         for index, job in enumerate(jobs):
-            groups.setdefault(_group_key(job, precision), []).append(index)
+            flags = _fast_flags(rows[index], job, precision) if allow_fast else 0
+            groups.setdefault(_group_key(job, precision) + (flags,), []).append(index)
         compute_units = _compute_units(self.device)
         passes = 2 if precision == "fp16x2" else (4 if precision == "fp32" else 1)
         store_cost = float(_config_value(self.config, "store_cost"))
         launches_planned = []
         for key, members in groups.items():
-            kind = key[0]
+            kind, group_flags = key[0], key[-1]
             tiles = _tiles(members, jobs)
             first = jobs[members[0]]
             channels, head_dim = first.channels, first.destination.head_dim
@@ -1327,12 +1375,14 @@ class _CallPlan:
             blocks_per_tile = (channels + 31) // 32
             max_ksteps = max((jobs[i].rank + 15) // 16 for i in members)
             steps = np.array([(jobs[i].rank + 15) // 16 for i in tiles[:, 0]], dtype=np.float64)
-            per_cu = self.config.get("workgroups_per_cu") or _occupancy(self.code, kind, max_ksteps)
+            per_cu = self.config.get("workgroups_per_cu") or _occupancy(self.code, kind, max_ksteps, head_dim, out_dtype,
+                                                                        group_flags)
             grid = int(max(1, min(len(tiles) * blocks_per_tile, compute_units * max(1, per_cu))))
             bounds = _balanced_bounds(steps * passes + store_cost, blocks_per_tile, grid)
             launches_planned.append(("restore", tile_offset, len(tiles), arena.add(bounds), grid, channels, head_dim,
-                                     kind, out_dtype, max_ksteps))
+                                     kind, out_dtype, max_ksteps, group_flags))
             self.grids.append(grid)
+            self.variants.append("fast" if group_flags & _lib.GF_FAST else "general")
         bound_tiles = _tiles(bound_jobs, jobs) if bound_jobs else None
         bound_tile_offset = arena.add(bound_tiles) if bound_jobs else None
         packs_offset = arena.add(pack_desc) if n_packs else None
@@ -1356,7 +1406,8 @@ class _CallPlan:
         if stage_events is not None:
             stage_events.append(("start", _record(self.stream)))
         if n_packs:
-            _lib.call("rch_basis_pack", base + packs_offset, n_packs, int(max(nblocks)), self.code, hip_stream)
+            _lib.call("rch_basis_pack", base + packs_offset, n_packs, int(max(nblocks)),
+                      int(max((packs[key] + 15) // 16 for key in pack_keys)), self.code, hip_stream)
             launches += 1
         if stage_events is not None:
             stage_events.append(("pack", _record(self.stream)))
@@ -1370,10 +1421,11 @@ class _CallPlan:
                 _lib.call("rch_rope_store", base + desc_offset, len(jobs), base + tile_offset, n_tiles, channels,
                           head_dim, out_dtype, hip_stream)
             else:
-                _, tile_offset, n_tiles, bounds_offset, grid, channels, head_dim, kind, out_dtype, max_ksteps = plan
+                (_, tile_offset, n_tiles, bounds_offset, grid, channels, head_dim, kind, out_dtype, max_ksteps,
+                 group_flags) = plan
                 _lib.call("rch_restore", base + desc_offset, len(jobs), base + tile_offset, n_tiles,
                           base + bounds_offset, grid, channels, head_dim, kind, out_dtype, self.code, max_ksteps,
-                          scratch_base, hip_stream)
+                          group_flags, scratch_base, hip_stream)
             launches += 1
         if stage_events is not None:
             stage_events.append(("fused", _record(self.stream)))
@@ -1448,7 +1500,7 @@ def _merged_config(config):
 def _run_hip(jobs, *, precision, config, stream, device, keepalive, stage_events):
     plan = _CallPlan(list(jobs), device, stream, precision, config, keepalive)
     launches = plan.run(stage_events)
-    return launches, plan.grids
+    return launches, plan.grids, plan.variants
 
 
 class _null:
@@ -1548,12 +1600,14 @@ def reconstruct(jobs, *, backend="auto", precision="auto", stream=None, wait_eve
                                   native_rope_dtype=native_rope_dtype)
     else:
         merged = _merged_config(config)
-        grids = []
+        grids, variants = [], []
 
         def run(selected):
-            launches, group_grids = _run_hip(selected, precision=precision, config=merged, stream=stream,
-                                             device=device, keepalive=keepalive, stage_events=stage_events)
+            launches, group_grids, group_variants = _run_hip(selected, precision=precision, config=merged,
+                                                             stream=stream, device=device, keepalive=keepalive,
+                                                             stage_events=stage_events)
             grids.extend(group_grids)
+            variants.extend(group_variants)
             return launches
 
         exact = [job for job in jobs if native_rope is not None and job.rope is not None]
@@ -1572,6 +1626,7 @@ def reconstruct(jobs, *, backend="auto", precision="auto", stream=None, wait_eve
                 _DEFERRED.append((failed, keepalive))
             raise
         stats["grids"] = grids
+        stats["variants"] = variants
     event = None
     if cuda:
         event = torch.cuda.Event()

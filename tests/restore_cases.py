@@ -53,8 +53,11 @@ def destination(layout, tokens, heads, head_dim, dtype, device, *, offset=0, ext
 
 def make_case(rng, *, grid, heads, head_dim, rank, basis_rows=None, source="uint8", rope="separable",
               layout="BTHD", out_dtype="bfloat16", device="cpu", basis_dtype=torch.float16, token_offset=0,
-              view=None, basis=None, table=None, rope_rows=None, coefficient_dtype=torch.float32):
-    """One job with random inputs; ``view`` (a NativeView) overrides the destination."""
+              view=None, basis=None, table=None, rope_rows=None, coefficient_dtype=torch.float32, code_pitch=None):
+    """One job with random inputs; ``view`` (a NativeView) overrides the destination.
+
+    ``code_pitch``: uint8 codes live in the first ``rank`` columns of ``[N, code_pitch]`` rows
+    whose padding holds nonzero bytes (they must not leak into the product)."""
     tokens = int(np.prod(grid))
     channels = heads * head_dim
     if basis is None:
@@ -69,7 +72,12 @@ def make_case(rng, *, grid, heads, head_dim, rank, basis_rows=None, source="uint
         scale, offset = random_affine(rank, rng)
         coefficients = orc.dequantize(codes, scale, offset)
         if source == "uint8":
-            src = rk.CoefficientSource(torch.from_numpy(codes).to(device), scale, offset)
+            stored = codes
+            if code_pitch is not None:
+                stored = np.full((tokens, code_pitch), 0xA5, dtype=np.uint8)
+                stored[:, :rank] = codes
+            values = torch.from_numpy(stored).to(device)[:, :rank]
+            src = rk.CoefficientSource(values, scale, offset)
         else:
             layout_v1 = oq.video_layout(grid[0], grid[1], grid[2], rank, "yuv444p")
             canvas, indices = orc.pack_pictures(codes, layout_v1, origin=(2, 3))

@@ -1,0 +1,105 @@
+"""GPU parity of the straight-line restore kernel (csrc/restore_fast.h).
+
+Launch groups whose jobs all qualify (uint8 codes in 16-byte aligned rows or pictures,
+head_dim % 32 == 0, unit-stride aligned destinations) run the straight-line kernel; every
+case here runs the same inputs once through it and once through the general kernel
+(``config={"fast_variant": False}``) and requires equal values, then checks both against the
+oracle's elementwise error bound (reelcache/restore_kernels.py:1208-1227).
+"""
+
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import restore as orc
+from reelcache_amd import restore_kernels as rk
+
+from restore_cases import destination, expected, make_case, written
+
+pytestmark = pytest.mark.gpu
+
+# (layout, heads, head_dim, rank, rope, grid, token_offset, code_pitch)
+SHAPES = [
+    ("BTHD", 3, 128, 128, "separable", (3, 7, 11), 5, None),   # ragged last tile (231 tokens)
+    ("THD", 2, 64, 33, "dense", (2, 9, 13), 0, 48),             # rank tail inside a 16-byte group
+    ("BHTD", 4, 64, 150, "none", (1, 16, 8), 2, 160),            # exactly one tile
+    ("BTHD", 12, 128, 192, "none", (1, 20, 26), 0, None),        # V-shaped, 5 tiles
+    ("BTHD", 1, 96, 7, "separable", (2, 3, 5), 1, 16),           # tiny rank, 30 tokens
+]
+
+
+def _pair(seed, precision, out_dtype, shape, device):
+    layout, heads, head_dim, rank, rope, grid, token_offset, pitch = shape
+    cases = []
+    for _ in range(2):
+        rng = np.random.default_rng(seed)
+        cases.append(make_case(rng, grid=grid, heads=heads, head_dim=head_dim, rank=rank, source="uint8",
+                               rope=rope, layout=layout, out_dtype=out_dtype, device=device,
+                               token_offset=token_offset, code_pitch=pitch))
+    return cases
+
+
+def _run(case, precision, fast):
+    handle = rk.reconstruct([case.job], precision=precision, config={"fast_variant": fast})
+    handle.release()
+    return handle.stats["variants"]
+
+
+def _check_bound(case, precision):
+    values, bound = expected(case, precision)
+    excess = np.abs(written(case) - values) - bound
+    assert float(excess.max()) <= 0, f"{int((excess > 0).sum())} elements exceed the error bound"
+
+
+@pytest.mark.parametrize("precision", ["fp16x2", "fp16", "bf16"])
+@pytest.mark.parametrize("out_dtype", ["bfloat16", "float16", "float32"])
+def test_fast_matches_general_and_oracle(device, precision, out_dtype):
+    for index, shape in enumerate(SHAPES):
+        seed = zlib.crc32(f"{precision}/{out_dtype}/{index}".encode())
+        fast, general = _pair(seed, precision, out_dtype, shape, device)
+        assert _run(fast, precision, True) == ["fast"], shape
+        assert _run(general, precision, False) == ["general"], shape
+        out_fast, out_general = written(fast), written(general)
+        assert np.array_equal(out_fast, out_general), f"{shape}: fast and general kernels differ"
+        _check_bound(fast, precision)
+        # Tokens outside the slot are untouched.
+        layout, token_offset = shape[0], shape[6]
+        tensor = fast.job.destination.tensor
+        canonical = (tensor.transpose(1, 2) if layout == "BHTD" else tensor).reshape(-1, shape[1] * shape[2])
+        tokens = int(np.prod(shape[5]))
+        assert bool((canonical[:token_offset] == -123.0).all())
+        assert bool((canonical[token_offset + tokens:] == -123.0).all())
+
+
+def test_fast_pictures_and_mixed_groups(device):
+    """Pictures and uint8 sources, K (RoPE) and V (none) jobs in one call: the call splits into
+    one straight-line launch per (source kind, RoPE) group."""
+    rng = np.random.default_rng(31)
+    table = rk.RopeTable.from_complex(torch.from_numpy(orc.wan_freqs(64, 64)))
+    heads, head_dim, grid, tokens = 4, 64, (2, 12, 14), 336
+    cache_k = destination("BTHD", 2 * tokens, heads, head_dim, "bfloat16", device)
+    cache_v = destination("BTHD", 2 * tokens, heads, head_dim, "bfloat16", device)
+    cases = []
+    for chunk in range(2):
+        cases.append(make_case(rng, grid=grid, heads=heads, head_dim=head_dim, rank=96, source="pictures",
+                               view=rk.NativeView(cache_k, token_offset=chunk * tokens), table=table,
+                               rope_rows=(2 * chunk, 0, 0), out_dtype="bfloat16", device=device))
+        cases.append(make_case(rng, grid=grid, heads=heads, head_dim=head_dim, rank=160, source="uint8",
+                               view=rk.NativeView(cache_v, token_offset=chunk * tokens), rope="none",
+                               out_dtype="bfloat16", device=device))
+    handle = rk.reconstruct([case.job for case in cases])
+    handle.release()
+    assert sorted(handle.stats["variants"]) == ["fast", "fast"]
+    for case in cases:
+        _check_bound(case, "fp16x2")
+
+
+def test_unaligned_jobs_use_the_general_kernel(device):
+    rng = np.random.default_rng(37)
+    case = make_case(rng, grid=(1, 5, 7), heads=2, head_dim=64, rank=33, source="uint8", device=device)
+    handle = rk.reconstruct([case.job])
+    handle.release()
+    assert handle.stats["variants"] == ["general"]  # rows of 33 bytes are not 16-byte aligned
+    _check_bound(case, "fp16x2")
