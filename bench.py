@@ -37,6 +37,7 @@ RANK_K, RANK_V = 128, 192
 CHANNELS = HEADS * HEAD_DIM
 TOKENS = GRID[0] * GRID[1] * GRID[2]
 HISTORY = CHUNKS * TOKENS
+COPY_PROBE_BYTES = 256 << 20
 METRIC = "restored KV GB/s + per-layer restore latency (CausVid shape, 1 GPU); fit chunks/s"
 
 
@@ -48,6 +49,22 @@ def layer_bytes():
     basis = (RANK_K + RANK_V) * CHANNELS * 2
     affine = CHUNKS * (RANK_K + RANK_V) * 2 * 4
     return written, written + codes + basis + affine
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "restore_causvid_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per layer call from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+    (copy-calibrated counters; counters cannot be read from inside this process), or None."""
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None
+    for line in text.splitlines():
+        if line.startswith("traffic_bytes_per_layer_call:"):
+            return int(line.split(":", 1)[1])
+    return None
 
 
 def layer_flops():
@@ -156,6 +173,9 @@ def main():
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--cpu-seconds", type=float, default=20.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--copy-probe", action="store_true",
+                        help="after the timed region, run 3 plain device copies of 256 MiB (the calibration "
+                             "dispatches for rocprofv3 FETCH_SIZE / WRITE_SIZE passes)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; the restore shards by layer or head with no "
@@ -214,12 +234,21 @@ def main():
         "wall_s": round(wall, 3),
         "host_us_per_layer_call": round(enqueued / (args.steps * LAYERS) * 1e6, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "traffic_source": "profiles/restore_causvid_traffic.md (rocprofv3 FETCH_SIZE + WRITE_SIZE per "
+                                       "layer call, calibrated on a 256 MiB copy)",
                      "kernel": "basis pack + restore launches per layer call: " + ", ".join(variants),
                      "algorithmic_bytes_per_launch": algorithmic,
                      "mfma_tflops": round(2 * layer_flops() / (kernel_avg / 1e3) / 1e12, 1)},
         "fit_chunks_per_s": None,
     }
+    if args.copy_probe:
+        source = torch.empty(COPY_PROBE_BYTES, dtype=torch.uint8, device=device).fill_(7)
+        target = torch.empty_like(source)
+        for _ in range(3):
+            target.copy_(source)
+        torch.cuda.synchronize(device)
+        del source, target
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(result), flush=True)

@@ -433,9 +433,12 @@ class RopeTable:
         entry = self._device_cache[cos.device]
         if entry.pairs is None:
             with torch.inference_mode(False), torch.no_grad():
-                stream = torch.cuda.current_stream(cos.device) if stream is None else stream
-                with torch.cuda.stream(stream):
+                if cos.device.type != "cuda":
                     entry.pairs = torch.stack((cos, sin), dim=-1).contiguous()
+                else:
+                    stream = torch.cuda.current_stream(cos.device) if stream is None else stream
+                    with torch.cuda.stream(stream):
+                        entry.pairs = torch.stack((cos, sin), dim=-1).contiguous()
         return entry.pairs
 
 
