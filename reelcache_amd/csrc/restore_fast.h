@@ -36,8 +36,16 @@ struct Cursor {
     int tile, bp, head;
 };
 
+// Largest number of 32-channel blocks (channels / 32) the straight-line kernel accepts.
+constexpr int kFastMaxBlocks = 256;
+
+// Three resident workgroups per CU where the LDS footprint allows it (KS <= 12: at most
+// 51 KB each) and the step fits the 168-VGPR budget that implies without spills (the two
+// RoPE pair sets add 32 VGPRs, so RoPE variants get three only up to KS = 8).
+template <int KS, bool ROPE> constexpr int kFastOccupancy = ((KS <= 12 && !ROPE) || (KS <= 8 && ROPE)) ? 3 : 2;
+
 template <int PREC, int KS, bool ROPE, int OUT>
-__global__ void __launch_bounds__(kThreads, 2)
+__global__ void __launch_bounds__(kThreads, (kFastOccupancy<KS, ROPE>))
 restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict__ tiles,
                     const int32_t* __restrict__ bounds, const int32_t* __restrict__ scratch, int heads,
                     int head_dim) {
@@ -53,6 +61,7 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
     __shared__ u4 lds[2][kBuffer];
     __shared__ __attribute__((aligned(16))) uint8_t codes[kTileTokens * kPitch];
     __shared__ __attribute__((aligned(16))) float affine[2 * kRanks];
+    __shared__ int block_exp[kFastMaxBlocks];  // basis block exponents of the current tile's job
 
     const int range = xcd_unit(blockIdx.x, gridDim.x);
     const int first_unit = bounds[range];
@@ -79,19 +88,25 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
     };
 
     // Basis fragments of a step: thread loads fragments q = tid + i * 256 of the step's block
-    // (zero beyond the job's rank).
+    // (zero beyond the job's rank).  The pack of the fetched tile's job is looked up only when
+    // the fetch cursor enters a new tile.
+    int fetch_tile = -1, fetch_ks = 0, fetch_nblocks = 0;
+    __amdgpu_buffer_rsrc_t pack = make_rsrc(0, 0);
     auto fetch = [&](const Cursor& c, u4 (&into)[kPer]) __attribute__((always_inline)) {
-        const rch_job* J = jobs + tiles[2 * c.tile];
-        const int ks = static_cast<int>((J->rank + 15) >> 4);
-        const int nblocks = static_cast<int>(J->pack_nblocks);
-        const __amdgpu_buffer_rsrc_t pack = make_rsrc(J->pack_ptr, int64_t(ks) * nblocks * 1024);
+        if (c.tile != fetch_tile) {
+            const rch_job* J = jobs + tiles[2 * c.tile];
+            fetch_ks = static_cast<int>((J->rank + 15) >> 4);
+            fetch_nblocks = static_cast<int>(J->pack_nblocks);
+            pack = make_rsrc(J->pack_ptr, int64_t(fetch_ks) * fetch_nblocks * 1024);
+            fetch_tile = c.tile;
+        }
         const uint32_t block_offset = static_cast<uint32_t>((c.head * head_blocks + c.bp) * 1024);
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
             const int q = tid + i * kThreads;
             const int s = q >> 6, li = q & 63;
-            const uint32_t offset = s < ks
-                                        ? static_cast<uint32_t>(s * nblocks) * 1024u + block_offset + li * 16
+            const uint32_t offset = s < fetch_ks
+                                        ? static_cast<uint32_t>(s * fetch_nblocks) * 1024u + block_offset + li * 16
                                         : kOutOfRange;
             into[i] = __builtin_amdgcn_raw_buffer_load_b128(pack, offset, 0, 0);
         }
@@ -102,16 +117,52 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
     };
 
     // Per-lane state of the current tile.
-    int current = -1;
     uint32_t dst_lane = kOutOfRange;  // byte offset of this lane's 16 channels of (token, head 0, dim 0)
     uint32_t row_t = 0, row_h = 0, row_w = 0;  // byte offsets of this token's RoPE rows
     __amdgpu_buffer_rsrc_t dst = make_rsrc(0, 0), pairs = make_rsrc(0, 0);
-    int coef_exp = 0, sec0 = 0, sec1 = 0;
+    int coef_exp = 0, sec0 = 0, sec1 = 0, head_bytes = 0;
     CoefFrag<PREC> cf[KS];
+
+    f4 rope_next[4], rope_now[4];  // RoPE pairs of the next / current dim block
+
+    // (cos, sin) of this lane's 8 pairs j = j0 .. j0 + 7 of a dim block (j0 = 16 bp + 8 h):
+    // into[p] = (cos, sin) of pairs j0 + 2p and j0 + 2p + 1.  A pair's table row depends on its
+    // section.  Dim blocks whose pairs all keep their section across each load's two pairs use
+    // four 16-byte loads; a block where a section boundary splits such a load (Wan: the odd
+    // boundary, one block per head) loads its pairs one by one.  The test is uniform.
+    auto rope_load = [&](int bp, f4 (&into)[4]) __attribute__((always_inline)) {
+        const int jb = 16 * bp;
+        // Row of pair j: row_t, plus (row_h - row_t) from section 1 on, plus (row_w - row_h) from
+        // section 2 on (written as adds of selected deltas: a three-way select of the rows is
+        // turned into a lookup table in scratch memory).
+        const uint32_t rt = row_t, d1 = row_h - row_t, d2 = row_w - row_h;
+        const int s0 = __builtin_amdgcn_readfirstlane(sec0), s1 = __builtin_amdgcn_readfirstlane(sec1);
+        auto row_of = [&](int j) __attribute__((always_inline)) {
+            return rt + (j >= s0 ? d1 : 0u) + (j >= s1 ? d2 : 0u);
+        };
+        // An odd section boundary inside [jb, jb + 16) splits a two-pair load.
+        const bool split = ((s0 & 1) && s0 > jb && s0 < jb + 16) || ((s1 & 1) && s1 > jb && s1 < jb + 16);
+        const int j0 = jb + 8 * h;
+        if (!split) {
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const int j = j0 + 2 * p;
+                into[p] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(pairs, row_of(j) + static_cast<uint32_t>(j * 8), 0, 0));
+            }
+        } else {
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const int j = j0 + 2 * p;
+                const u2 a = __builtin_amdgcn_raw_buffer_load_b64(pairs, row_of(j) + static_cast<uint32_t>(j * 8), 0, 0);
+                const u2 b = __builtin_amdgcn_raw_buffer_load_b64(pairs, row_of(j + 1) + static_cast<uint32_t>((j + 1) * 8), 0, 0);
+                into[p] = f4{__uint_as_float(a[0]), __uint_as_float(a[1]), __uint_as_float(b[0]), __uint_as_float(b[1])};
+            }
+        }
+    };
 
     // Tile entry: stage the tile's codes and affine in LDS, convert this wave's 32 tokens to
     // coefficient fragments.  All waves passed a barrier since they last read codes / affine.
-    auto enter = [&](const rch_job* J, int t0) __attribute__((always_inline)) {
+    auto enter = [&](const rch_job* J, int t0, int first_bp) __attribute__((always_inline)) {
         const int64_t tokens = J->tokens;
         const int64_t t = t0 + wave * 32 + col;
         const bool valid = t < tokens;
@@ -131,10 +182,15 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
             row_w = dense ? first : third;
             sec0 = static_cast<int>(J->sec_t);
             sec1 = static_cast<int>(J->sec_t + J->sec_h);
+            // Pairs of the tile's first dim block, issued before the code loads so that the
+            // drain below covers them.
+            rope_load(first_bp, rope_now);
         }
         coef_exp = kFp16 ? static_cast<int>(J->coef_exp) : 0;
+        head_bytes = static_cast<int>(J->dst_head_stride) * kEsize;
         const float pre = pow2f(coef_exp);
         const int rank = static_cast<int>(J->rank);
+        for (int i = tid; i < per_tile; i += kThreads) block_exp[i] = scratch[J->basis_exp_index + i];
         if (J->pic_slots == 0) {  // uint8 rows, 16-byte aligned
             const int64_t rs = J->src_row_stride;
             constexpr int kGroups = kRanks / 16;
@@ -214,37 +270,34 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
         }
     };
 
-    // (cos, sin) of this lane's 8 pairs j = 16 bp + 8 h + p of a dim block.  A pair's table row
-    // depends on its section: the section tests are uniform per lane half, so they reduce to
-    // scalar masks and one select per pair.
-    auto rope_load = [&](int bp, u2 (&into)[8]) __attribute__((always_inline)) {
-        const int jb = 16 * bp;
-        const uint32_t rt = row_t, rh = row_h, rw = row_w;  // values: a select of lvalues selects addresses
-#pragma unroll
-        for (int p = 0; p < 8; ++p) {
-            const bool in_t = h ? (jb + 8 + p < sec0) : (jb + p < sec0);
-            const bool in_h = h ? (jb + 8 + p < sec1) : (jb + p < sec1);
-            const uint32_t row = in_t ? rt : (in_h ? rh : rw);
-            into[p] = __builtin_amdgcn_raw_buffer_load_b64(pairs, row + static_cast<uint32_t>((jb + 8 * h + p) * 8), 0, 0);
-        }
-    };
-
     // One step: product of the staged block, scale, RoPE, cast, store.
-    auto finish = [&](const rch_job* J, const Cursor& c, int buffer, const u2 (&rope)[8]) __attribute__((always_inline)) {
+    auto finish = [&](const Cursor& c, int buffer, const f4 (&rope)[4]) __attribute__((always_inline)) {
+        // Undo the coefficient prescale and the block's basis exponent (exact powers of two).
+        const int e = coef_exp + block_exp[c.head * head_blocks + c.bp];
+        // Basis fragments are read from LDS three steps ahead of their products (a rotating
+        // window of four registers).
+        constexpr int kAhead = 3;
+        const u4* frags = &lds[buffer][lane];
+        u4 window[kAhead + 1];
+#pragma unroll
+        for (int j = 0; j < kAhead; ++j) window[j] = frags[j * kStepFrags];
         f16v acc = {};
 #pragma unroll
-        for (int s = 0; s < KS; ++s) acc = mfma_step<PREC>(&lds[buffer][s * kStepFrags + lane], cf[s], acc);
-        // Undo the coefficient prescale and the block's basis exponent (exact powers of two).
-        const int e = coef_exp + scratch[J->basis_exp_index + c.head * head_blocks + c.bp];
+        for (int s = 0; s < KS; ++s) {
+            if (s + kAhead < KS) window[(s + kAhead) % (kAhead + 1)] = frags[(s + kAhead) * kStepFrags];
+            acc = mfma_frag<PREC>(window[s % (kAhead + 1)], cf[s], acc);
+        }
         float v[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) v[i] = __builtin_amdgcn_ldexpf(acc[i], -e);
         if constexpr (ROPE) {
 #pragma unroll
-            for (int p = 0; p < 8; ++p)
-                rotate(v[2 * p], v[2 * p + 1], __uint_as_float(rope[p][0]), __uint_as_float(rope[p][1]));
+            for (int p = 0; p < 4; ++p) {
+                rotate(v[4 * p], v[4 * p + 1], rope[p][0], rope[p][1]);
+                rotate(v[4 * p + 2], v[4 * p + 3], rope[p][2], rope[p][3]);
+            }
         }
-        const uint32_t offset = dst_lane + static_cast<uint32_t>((c.head * J->dst_head_stride + c.bp * 32) * kEsize);
+        const uint32_t offset = dst_lane + static_cast<uint32_t>(c.head * head_bytes + c.bp * 32 * kEsize);
         if constexpr (OUT == RCH_DT_F32) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -282,40 +335,46 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
     }
     Cursor ahead1 = advance(now), ahead2 = advance(ahead1);
     u4 ring[kPer];
-    u2 rope_next[8], rope_now[8];
 
     fetch(now, ring);
     commit(0, ring);
     fetch(ahead1, ring);
-    // Stores at out-of-range offsets (dropped by the hardware) after the prologue's ring loads.
-    // The wait the compiler places before the commit is shared by every step and must also hold
-    // for the path from this prologue; a step issues up to 12 memory operations after its ring
-    // loads (8 RoPE loads, 4 stores), so with at least as many here that wait covers just the
-    // ring loads instead of draining the stores of the previous step.
+    // Loops: tile (entry: stage and convert the tile's coefficients; its loads drain the memory
+    // counter) > dim block (RoPE pairs change) > head (the steps: straight-line code whose only
+    // predecessors are the loop entry and its own back edge, so the waits the compiler places
+    // are the steady-state ones).  In step st the ring holds the fragments of step st + 1
+    // (fetched during step st - 1); they go to the other LDS buffer and the fragments of step
+    // st + 2 are fetched in their place.
+    int st = 0;
+    while (st < steps) {
+        const int tile = now.tile;
+        enter(jobs + tiles[2 * tile], tiles[2 * tile + 1], now.bp);
+        while (st < steps && now.tile == tile) {
+            // RoPE pairs of the next dim block are fetched at the start of this one and copied at
+            // the end of its last step: the wait before the copy follows a fixed number of memory
+            // operations (it covers loads only; waiting for a store to complete costs
+            // microseconds under this write stream), and the loads have the whole dim block to
+            // arrive (a load queues behind the stores issued before it).
+            if constexpr (ROPE) {
+                if (now.bp + 1 < head_blocks) rope_load(now.bp + 1, rope_next);
+            }
+            const int run = min(heads - now.head, steps - st);
+            for (int i = 0; i < run; ++i, ++st) {
+                commit((st + 1) & 1, ring);
+                fetch(ahead2, ring);
+                finish(now, st & 1, rope_now);
+                __syncthreads();
+                if constexpr (ROPE) {
+                    if (i + 1 == run) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) __builtin_amdgcn_raw_buffer_store_b32(0u, dst, kOutOfRange + 4 * i, 0, 0);
-    // Step st: the ring holds the fragments of step st + 1 (fetched during step st - 1); they go
-    // to the other LDS buffer, and the fragments of step st + 2 are fetched in their place.
-    // Each wait for the ring therefore covers loads issued a whole step earlier and none of the
-    // stores issued after them.
-    for (int st = 0; st < steps; ++st) {
-        const rch_job* J = jobs + tiles[2 * now.tile];
-        if (now.tile != current) {  // the first step enters its tile here too
-            enter(J, tiles[2 * now.tile + 1]);
-            current = now.tile;
-            if constexpr (ROPE) rope_load(now.bp, rope_now);
-        } else if constexpr (ROPE) {
-#pragma unroll
-            for (int p = 0; p < 8; ++p) rope_now[p] = rope_next[p];
+                        for (int p = 0; p < 4; ++p) rope_now[p] = rope_next[p];
+                    }
+                }
+                now = ahead1;
+                ahead1 = ahead2;
+                ahead2 = advance(ahead2);
+            }
         }
-        commit((st + 1) & 1, ring);
-        fetch(ahead2, ring);
-        if constexpr (ROPE) rope_load(ahead1.bp, rope_next);
-        finish(J, now, st & 1, rope_now);
-        __syncthreads();
-        now = ahead1;
-        ahead1 = ahead2;
-        ahead2 = advance(ahead2);
     }
 }
 

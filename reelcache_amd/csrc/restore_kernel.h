@@ -134,6 +134,20 @@ __device__ __forceinline__ f16v mfma_step(const u4* frag, const CoefFrag<PREC>& 
     return acc;
 }
 
+// One 16-rank step from a basis fragment already in registers (16-bit modes).
+template <int PREC>
+__device__ __forceinline__ f16v mfma_frag(u4 frag, const CoefFrag<PREC>& c, f16v acc) {
+    static_assert(PREC != RCH_PREC_FP32, "fp32 fragments are 32 bytes");
+    if constexpr (PREC == RCH_PREC_BF16) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf8, frag), c.hi, acc, 0, 0, 0);
+    } else {
+        const h8 a = __builtin_bit_cast(h8, frag);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, c.hi, acc, 0, 0, 0);
+        if constexpr (PREC == RCH_PREC_FP16X2) acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, c.lo, acc, 0, 0, 0);
+        return acc;
+    }
+}
+
 // RoPE table row of pair j for a token (separable sections or dense rows).
 __device__ __forceinline__ int64_t rope_row(const rch_job* J, int kind, int j, int64_t t, int f, int y, int x) {
     if (kind == RCH_ROPE_DENSE) return J->row_t + t;
