@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-#define RCH_ABI_VERSION 2
+#define RCH_ABI_VERSION 3
 
 /* Status codes (mapped to reelcache errors by the host). */
 #define RCH_OK 0
@@ -182,6 +182,96 @@ int rch_restore_occupancy(int precision, int source_kind, int max_ksteps, int he
  */
 int rch_rope_store(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev, int n_tiles,
                    int channels, int head_dim, int out_dtype, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Fit side (reelcache/gpu_fitting.py, reelcache/factorization.py, reelcache/node_packets.py).
+ * ------------------------------------------------------------------------------------------ */
+
+/*
+ * One [rows, channels] source matrix X of a batched fit call, with its stored fp16 basis Q,
+ * its fp32 coefficients P = X Q[:rank]^T and per-matrix device outputs.  Fields an entry point
+ * does not use may be 0.  All pointers are device byte addresses, strides are in elements, and
+ * every row has unit column stride.  X rows start 16-byte aligned (src_stride * element size
+ * % 16 == 0) and channels % 8 == 0; the host pads other shapes with zero channels.
+ */
+typedef struct rch_fit_matrix {
+    int64_t src_ptr;      /* X [rows, >= channels] */
+    int64_t src_dtype;    /* RCH_DT_F32 / RCH_DT_F16 / RCH_DT_BF16 (one dtype per call) */
+    int64_t rows;
+    int64_t src_stride;
+    int64_t basis_ptr;    /* fp16 Q [>= rank, channels] */
+    int64_t basis_stride;
+    int64_t rank;         /* 0: no basis (source energy only) */
+    int64_t coef_ptr;     /* fp32 P [rows, >= rank]; coef_stride % 4 == 0, 16-byte aligned */
+    int64_t coef_stride;
+    int64_t gram_ptr;     /* fp32 G [channels, >= channels]; gram_stride % 4 == 0, 16-byte aligned */
+    int64_t gram_stride;
+    int64_t absmax_ptr;   /* uint32: fp32 bits of max|X| (zero-filled, then rch_fit_absmax) */
+    int64_t extrema_ptr;  /* uint32 [2, rank]: ~key(min) then key(max) of each column of P, or 0 */
+    int64_t energy_ptr;   /* float64 [2]: sum (X/s)^2 and sum ((X - P Q)/s)^2, s = max|X| */
+    int64_t partial_ptr;  /* float64 [ceil(rows / 64), 2]: per-64-row partial energies */
+    int64_t reserved;
+} rch_fit_matrix;         /* 16 x int64 = 128 bytes */
+
+int rch_fit_matrix_size(void);
+
+/*
+ * max|X| of each matrix as fp32 bits, combined with unsigned atomic max into *absmax_ptr
+ * (zero-filled by the caller).  A non-finite element yields bits >= 0x7f800000.
+ * Replaces `torch.maximum(tensor.amax().abs(), tensor.amin().abs())` and the finite scans of
+ * project_onto_basis / measure_source_energy (reelcache/factorization.py:343-349, :708-712).
+ */
+int rch_fit_absmax(const rch_fit_matrix* mats_dev, int n_mats, int channels, int64_t max_rows, int src_dtype,
+                   void* stream);
+
+/*
+ * Symmetric Gram G = X^T X of each matrix in fp32, both triangles written (exactly symmetric,
+ * so (G + G^T) / 2 == G).  16-bit sources run on v_mfma_f32_32x32x16_{bf16,f16} (exact
+ * products, fp32 accumulation), fp32 sources on v_mfma_f32_32x32x2f32.  Only the 128 x 128
+ * tiles of the lower triangle are computed.
+ * Replaces `torch.stack([mm(x.T, x) for x in sources])` + symmetrization of gram_bases and
+ * _symmetric_gram (reelcache/gpu_fitting.py:286-289, reelcache/rank_method.py:634-638).
+ */
+int rch_fit_gram(const rch_fit_matrix* mats_dev, int n_mats, int channels, int src_dtype, void* stream);
+
+/*
+ * Coefficients P = X Q[:rank]^T of each matrix: exact products accumulated in FP64 on
+ * v_mfma_f64_16x16x4f64, rounded once to fp32.  When extrema_ptr is set, also the per-column
+ * min / max of P as order-preserving keys (unsigned atomic max, zero-filled by the caller).
+ * Replaces `tensor.float() @ b32.T` of project_onto_basis (reelcache/factorization.py:384-392)
+ * and the extrema of quantize_device (reelcache/node_packets.py:164).
+ */
+int rch_fit_project(const rch_fit_matrix* mats_dev, int n_mats, int channels, int64_t max_rows, int max_rank,
+                    int src_dtype, void* stream);
+
+/*
+ * Direct residual and source energies of each matrix in FP64: sum (X / s)^2 and
+ * sum ((X - P Q[:rank]) / s)^2 with s = max|X| read from *absmax_ptr (no scaling when s == 0),
+ * the reconstruction accumulated in FP64 on v_mfma_f64_16x16x4f64.  Per-64-row partials go to
+ * partial_ptr and are summed in a fixed order into energy_ptr (deterministic).  rank == 0
+ * measures the source energy alone.
+ * Replaces the tiled residual guard of project_onto_basis (reelcache/factorization.py:398-419)
+ * and measure_source_energy (reelcache/factorization.py:692-724).
+ */
+int rch_fit_residual(const rch_fit_matrix* mats_dev, int n_mats, int channels, int64_t max_rows, int src_dtype,
+                     void* stream);
+
+/*
+ * Per-column extrema of an fp32 [rows, cols] matrix: keys[c] = ~key(min), keys[cols + c] =
+ * key(max) (unsigned atomic max, zero-filled by the caller), key = order-preserving fp32 bits.
+ * Replaces `torch.stack((coefficients.amin(0), coefficients.amax(0)))` of quantize_device
+ * (reelcache/node_packets.py:164).
+ */
+int rch_column_extrema(const float* values_dev, int64_t rows, int cols, int64_t stride, uint32_t* keys_dev,
+                       void* stream);
+
+/*
+ * 8-bit quantization: codes[r, c] = clamp(rint((double(v) - offset[c]) / scale[c]), 0, 255), 0 where
+ * scale[c] == 0, in FP64 (round half to even).  Replaces the device arithmetic of quantize_device
+ * (reelcache/node_packets.py:166-172) = _hevc.quantize_coefficients (reelcache/_hevc.py:465-472).
+ */
+int rch_quantize(const float* values_dev, int64_t rows, int cols, int64_t stride, const double* scale_dev,
+                 const double* offset_dev, uint8_t* codes_dev, int64_t code_stride, void* stream);
 
 #ifdef __cplusplus
 }

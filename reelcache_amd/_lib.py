@@ -16,7 +16,7 @@ import numpy as np
 from .errors import ConfigurationError, UnsupportedError
 
 LIBRARY = Path(__file__).resolve().with_name("libreelcache_hip.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # Status codes (RCH_E_*).
 OK, E_CONFIG, E_UNSUPPORTED, E_LAUNCH = 0, 1, 2, 3
@@ -45,6 +45,11 @@ JOB_DTYPE = np.dtype([(name, "<i8") for name in JOB_FIELDS])
 PACK_FIELDS = ("src_ptr", "src_dtype", "row_stride", "rank", "channels", "dst_ptr", "ksteps", "nblocks",
                "reserved2", "exp_ptr", "reserved0", "reserved1")
 PACK_DTYPE = np.dtype([(name, "<i8") for name in PACK_FIELDS])
+# rch_fit_matrix field order (16 x int64).
+FIT_FIELDS = ("src_ptr", "src_dtype", "rows", "src_stride", "basis_ptr", "basis_stride", "rank", "coef_ptr",
+              "coef_stride", "gram_ptr", "gram_stride", "absmax_ptr", "extrema_ptr", "energy_ptr", "partial_ptr",
+              "reserved")
+FIT_DTYPE = np.dtype([(name, "<i8") for name in FIT_FIELDS])
 
 _i, _i64, _p = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
 _SIGNATURES = {
@@ -58,8 +63,15 @@ _SIGNATURES = {
     "rch_restore": ([_p, _i, _p, _i, _p, _i, _i, _i, _i, _i, _i, _i, _i, _p, _p], _i),
     "rch_restore_occupancy": ([_i, _i, _i, _i, _i, _i, ctypes.POINTER(_i)], _i),
     "rch_rope_store": ([_p, _i, _p, _i, _i, _i, _i, _p], _i),
+    "rch_fit_matrix_size": ([], _i),
+    "rch_fit_absmax": ([_p, _i, _i, _i64, _i, _p], _i),
+    "rch_fit_gram": ([_p, _i, _i, _i, _p], _i),
+    "rch_fit_project": ([_p, _i, _i, _i64, _i, _i, _p], _i),
+    "rch_fit_residual": ([_p, _i, _i, _i64, _i, _p], _i),
+    "rch_column_extrema": ([_p, _i64, _i, _i64, _p, _p], _i),
+    "rch_quantize": ([_p, _i64, _i, _i64, _p, _p, _p, _i64, _p], _i),
 }
-# Fit entry points are bound when present (declared in the same header).
+# Further entry points registered by other modules are bound when present.
 _OPTIONAL_SIGNATURES: dict = {}
 
 _LOCK = threading.Lock()
@@ -86,7 +98,8 @@ def _load():
             function.argtypes, function.restype = arguments, result
     if lib.rch_abi_version() != ABI_VERSION:
         raise UnsupportedError(f"{LIBRARY.name} has ABI {lib.rch_abi_version()}, expected {ABI_VERSION}; rebuild it")
-    if lib.rch_job_size() != JOB_DTYPE.itemsize or lib.rch_pack_size() != PACK_DTYPE.itemsize:
+    if (lib.rch_job_size() != JOB_DTYPE.itemsize or lib.rch_pack_size() != PACK_DTYPE.itemsize
+            or lib.rch_fit_matrix_size() != FIT_DTYPE.itemsize):
         raise UnsupportedError(f"{LIBRARY.name} descriptor layout differs from this package; rebuild it")
     return lib
 

@@ -6,7 +6,38 @@
 
 #include "../../include/reelcache_hip.h"
 
+#define RCH_GLOBAL __attribute__((address_space(1)))
+
 namespace rch {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef double d4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u4 __attribute__((ext_vector_type(4)));  // native vectors: promotable to registers
+typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+
+// Device addresses arrive as int64 descriptor fields; these views make the compiler emit
+// global (not flat) memory instructions.
+template <typename T>
+__device__ __forceinline__ const RCH_GLOBAL T* gin(int64_t address) {
+    return reinterpret_cast<const RCH_GLOBAL T*>(address);
+}
+template <typename T>
+__device__ __forceinline__ RCH_GLOBAL T* gout(int64_t address) {
+    return reinterpret_cast<RCH_GLOBAL T*>(address);
+}
+
+// Raw buffer resources: loads at offsets >= the record count return zero and stores there are
+// dropped, so out-of-range lanes need no branches.  kOutOfRange is an offset past any record count.
+constexpr int kBufferWord3 = 0x00020000;  // raw buffer resource word 3 for the gfx9 family
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(int64_t base, int64_t bytes) {
+    const int records = bytes > 0x7fffffff ? 0x7fffffff : static_cast<int>(bytes < 0 ? 0 : bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(base), 0, records, kBufferWord3);
+}
 
 // Records `message` as this thread's last error and returns `code`.
 int fail(int code, const char* format, ...) __attribute__((format(printf, 2, 3)));

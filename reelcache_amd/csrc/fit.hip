@@ -1,0 +1,626 @@
+// Fit-side kernels for MI355X (gfx950): max|X|, batched symmetric Gram, projection onto a
+// stored fp16 basis, direct residual / source energies, column extrema and the 8-bit quantizer.
+//
+// Reference: reelcache/gpu_fitting.py (gram_bases :276-295), reelcache/rank_method.py
+// (_symmetric_gram :634-638), reelcache/factorization.py (project_onto_basis :318-434,
+// measure_source_energy :692-724), reelcache/node_packets.py (quantize_device :155-173),
+// reelcache/_hevc.py (quantize_coefficients :445-472).
+//
+// Arithmetic contract:
+//   * Gram: exact products (16-bit sources on 16-bit MFMA, whose products are exact in fp32;
+//     fp32 sources on fp32 MFMA), fp32 accumulation, exactly symmetric output.
+//   * Projection P = X Q^T and the reconstruction P Q of the residual: operands converted
+//     exactly to FP64, products and sums on v_mfma_f64_16x16x4f64, P rounded once to fp32.
+//     The FP64 sum makes P the correctly rounded fp32 value of the exact dot product except
+//     within ~1e-13 relative of a rounding boundary, i.e. independent of summation order.
+//   * Energies: FP64 per element ((x - r) / s)^2, per-64-row partials, fixed-order totals.
+//   * Quantizer: FP64 (v - offset) / scale, round half to even, clamp to [0, 255].
+#include <type_traits>
+
+#include "common.h"
+
+namespace rch {
+namespace {
+
+constexpr int kThreads = 256;
+
+template <int DT>
+constexpr int esize() {
+    return DT == RCH_DT_F32 ? 4 : 2;
+}
+
+// 16-bit element bits -> float.
+template <int DT>
+__device__ __forceinline__ float half_bits(uint32_t bits) {
+    if constexpr (DT == RCH_DT_BF16) {
+        return __uint_as_float(bits << 16);
+    } else {
+        return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+    }
+}
+
+// Eight consecutive source elements as doubles.
+template <int DT>
+__device__ __forceinline__ void load8(__amdgpu_buffer_rsrc_t rsrc, uint32_t offset, double (&v)[8]) {
+    if constexpr (DT == RCH_DT_F32) {
+        const u4 a = __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, 0);
+        const u4 b = __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset + 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[i] = static_cast<double>(__uint_as_float(a[i]));
+            v[4 + i] = static_cast<double>(__uint_as_float(b[i]));
+        }
+    } else {
+        const u4 w = __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = static_cast<double>(half_bits<DT>(w[i] & 0xffffu));
+            v[2 * i + 1] = static_cast<double>(half_bits<DT>(w[i] >> 16));
+        }
+    }
+}
+
+// Order-preserving unsigned key of an fp32 value (larger value -> larger key).
+__device__ __forceinline__ uint32_t order_key(float v) {
+    const uint32_t u = __float_as_uint(v);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Buffer over rows [r0, rows) of a source matrix (empty when r0 >= rows).
+template <int DT>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t source_rows(const rch_fit_matrix* M, int channels, int64_t r0) {
+    constexpr int E = esize<DT>();
+    const int64_t left = M->rows - r0;
+    return make_rsrc(M->src_ptr + r0 * M->src_stride * E, left > 0 ? ((left - 1) * M->src_stride + channels) * E : 0);
+}
+
+// ---------------------------------------------------------------------------------------------
+// max|X|: workgroup (64-row tile, matrix); one unsigned atomic max of the fp32 bits per workgroup.
+// ---------------------------------------------------------------------------------------------
+
+template <int DT>
+__global__ void __launch_bounds__(kThreads) absmax_kernel(const rch_fit_matrix* __restrict__ mats, int channels) {
+    const rch_fit_matrix* M = mats + blockIdx.y;
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * 64;
+    if (r0 >= M->rows) return;
+    constexpr int E = esize<DT>();
+    const int rows = static_cast<int>(M->rows - r0 < 64 ? M->rows - r0 : 64);
+    const __amdgpu_buffer_rsrc_t src = source_rows<DT>(M, channels, r0);
+    const int groups = channels / 8;  // 8 elements per load
+    uint32_t m = 0;
+    for (int i = threadIdx.x; i < rows * groups; i += kThreads) {
+        const int r = i / groups, g = i - r * groups;
+        double v[8];
+        load8<DT>(src, static_cast<uint32_t>((r * M->src_stride + 8 * g) * E), v);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t bits = __float_as_uint(static_cast<float>(v[j])) & 0x7fffffffu;  // exact: v is a float
+            m = bits > m ? bits : m;
+        }
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        const uint32_t o = __shfl_xor(m, d);
+        m = o > m ? o : m;
+    }
+    __shared__ uint32_t part[kThreads / 64];
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < kThreads / 64; ++w) m = part[w] > m ? part[w] : m;
+        atomicMax(reinterpret_cast<unsigned int*>(M->absmax_ptr), m);  // vector atomic
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Gram G = X^T X.  Workgroup = one 128 x 128 tile (ti >= tj) of one matrix; 4 waves, each a
+// 64 x 64 quadrant as 2 x 2 MFMA 32x32 blocks.  Rows are staged 32 per step into LDS as
+// [channel][row]: each lane loads a channel pair of 8 rows (coalesced along the row) and
+// writes the two channels' 8-row runs, so that an MFMA operand (8 consecutive rows of one
+// channel for 16-bit sources, 16 for fp32) is one or four 16-byte LDS reads.
+// Register-prefetched, double-buffered LDS, one barrier per step.
+// ---------------------------------------------------------------------------------------------
+
+constexpr int kGramTile = 128;
+constexpr int kGramRows = 32;
+
+template <int DT>
+constexpr int gram_pitch() {
+    return DT == RCH_DT_F32 ? kGramRows * 4 + 16 : kGramRows * 2 + 16;  // bytes per staged channel
+}
+
+template <int DT>
+struct GramStage {
+    typedef typename std::conditional<DT == RCH_DT_F32, u2, uint32_t>::type word;
+    word d[8];  // rows r0 .. r0 + 7 of this lane's channel pair
+};
+
+template <int DT>
+__device__ __forceinline__ void gram_load(GramStage<DT>& st, const rch_fit_matrix* M, int channels, int64_t r0, int c) {
+    constexpr int E = esize<DT>();
+    const __amdgpu_buffer_rsrc_t src = source_rows<DT>(M, channels, r0);
+    const uint32_t offset = c < channels ? static_cast<uint32_t>(c * E) : kOutOfRange;
+    const uint32_t row_bytes = static_cast<uint32_t>(M->src_stride * E);
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        if constexpr (DT == RCH_DT_F32)
+            st.d[r] = __builtin_amdgcn_raw_buffer_load_b64(src, offset + r * row_bytes, 0, 0);
+        else
+            st.d[r] = __builtin_amdgcn_raw_buffer_load_b32(src, offset + r * row_bytes, 0, 0);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void gram_store(const GramStage<DT>& st, unsigned char* tile, int lane, int wave) {
+    constexpr int P = gram_pitch<DT>();
+    unsigned char* c0 = tile + (2 * lane) * P;
+    unsigned char* c1 = c0 + P;
+    if constexpr (DT == RCH_DT_F32) {
+        const u4 a0 = {st.d[0][0], st.d[1][0], st.d[2][0], st.d[3][0]};
+        const u4 a1 = {st.d[4][0], st.d[5][0], st.d[6][0], st.d[7][0]};
+        const u4 b0 = {st.d[0][1], st.d[1][1], st.d[2][1], st.d[3][1]};
+        const u4 b1 = {st.d[4][1], st.d[5][1], st.d[6][1], st.d[7][1]};
+        *reinterpret_cast<u4*>(c0 + 32 * wave) = a0;
+        *reinterpret_cast<u4*>(c0 + 32 * wave + 16) = a1;
+        *reinterpret_cast<u4*>(c1 + 32 * wave) = b0;
+        *reinterpret_cast<u4*>(c1 + 32 * wave + 16) = b1;
+    } else {
+        u4 lo, hi;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            lo[q] = (st.d[2 * q] & 0xffffu) | (st.d[2 * q + 1] << 16);
+            hi[q] = (st.d[2 * q] >> 16) | (st.d[2 * q + 1] & 0xffff0000u);
+        }
+        *reinterpret_cast<u4*>(c0 + 16 * wave) = lo;
+        *reinterpret_cast<u4*>(c1 + 16 * wave) = hi;
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void gram_mfma(f16v (&acc)[2][2], const unsigned char* ti, const unsigned char* tj, int wm,
+                                          int wn, int lane) {
+    constexpr int P = gram_pitch<DT>();
+    const int h = lane >> 5, col = lane & 31;
+    const unsigned char* a_base = ti + (wm * 64 + col) * P;
+    const unsigned char* b_base = tj + (wn * 64 + col) * P;
+    if constexpr (DT == RCH_DT_F32) {
+        // Lane half h holds rows 16h .. 16h + 15; MFMA step s takes row 16h + s.
+        f4 a[2][4], b[2][4];
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                a[x][q] = *reinterpret_cast<const f4*>(a_base + x * 32 * P + 64 * h + 16 * q);
+                b[x][q] = *reinterpret_cast<const f4*>(b_base + x * 32 * P + 64 * h + 16 * q);
+            }
+#pragma unroll
+        for (int s = 0; s < 16; ++s)
+#pragma unroll
+            for (int x = 0; x < 2; ++x)
+#pragma unroll
+                for (int y = 0; y < 2; ++y)
+                    acc[x][y] =
+                        __builtin_amdgcn_mfma_f32_32x32x2f32(a[x][s >> 2][s & 3], b[y][s >> 2][s & 3], acc[x][y], 0, 0, 0);
+    } else {
+        // Two 16-row steps; lane half h holds rows 16 ks + 8h .. + 7.
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            u4 a[2], b[2];
+#pragma unroll
+            for (int x = 0; x < 2; ++x) {
+                a[x] = *reinterpret_cast<const u4*>(a_base + x * 32 * P + 32 * ks + 16 * h);
+                b[x] = *reinterpret_cast<const u4*>(b_base + x * 32 * P + 32 * ks + 16 * h);
+            }
+#pragma unroll
+            for (int x = 0; x < 2; ++x)
+#pragma unroll
+                for (int y = 0; y < 2; ++y) {
+                    if constexpr (DT == RCH_DT_BF16)
+                        acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf8, a[x]),
+                                                                            __builtin_bit_cast(bf8, b[y]), acc[x][y], 0, 0, 0);
+                    else
+                        acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8, a[x]),
+                                                                           __builtin_bit_cast(h8, b[y]), acc[x][y], 0, 0, 0);
+                }
+        }
+    }
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kThreads) gram_kernel(const rch_fit_matrix* __restrict__ mats, int channels, int tiles,
+                                                        int grid) {
+    constexpr int P = gram_pitch<DT>();
+    __shared__ __attribute__((aligned(16))) unsigned char lds[2][2][kGramTile * P];
+
+    const int unit = xcd_unit(blockIdx.x, grid);  // the tiles of one matrix share an XCD's L2
+    const int mat = unit / tiles;
+    int ti = 0, rest = unit - mat * tiles;
+    while (rest > ti) {  // tile index -> (ti, tj), row-major over the lower triangle
+        rest -= ti + 1;
+        ++ti;
+    }
+    const int tj = rest;
+    const bool diagonal = ti == tj;
+    const rch_fit_matrix* M = mats + mat;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int ci = ti * kGramTile + 2 * lane, cj = tj * kGramTile + 2 * lane;
+    const int steps = static_cast<int>((M->rows + kGramRows - 1) / kGramRows);
+
+    f16v acc[2][2];
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < 2; ++y) acc[x][y] = f16v{};
+
+    GramStage<DT> si, sj;
+    gram_load<DT>(si, M, channels, 8 * wave, ci);
+    if (!diagonal) gram_load<DT>(sj, M, channels, 8 * wave, cj);
+    gram_store<DT>(si, lds[0][0], lane, wave);
+    if (!diagonal) gram_store<DT>(sj, lds[0][1], lane, wave);
+    __syncthreads();
+    for (int step = 0; step < steps; ++step) {
+        const int buf = step & 1;
+        const bool more = step + 1 < steps;
+        if (more) {
+            const int64_t r0 = static_cast<int64_t>(step + 1) * kGramRows + 8 * wave;
+            gram_load<DT>(si, M, channels, r0, ci);
+            if (!diagonal) gram_load<DT>(sj, M, channels, r0, cj);
+        }
+        gram_mfma<DT>(acc, lds[buf][0], diagonal ? lds[buf][0] : lds[buf][1], wm, wn, lane);
+        if (more) {
+            gram_store<DT>(si, lds[buf ^ 1][0], lane, wave);
+            if (!diagonal) gram_store<DT>(sj, lds[buf ^ 1][1], lane, wave);
+        }
+        __syncthreads();
+    }
+
+    // Accumulator element e of lane l: row 8 (e / 4) + 4 (l / 32) + e % 4, column l % 32.
+    RCH_GLOBAL float* G = gout<float>(M->gram_ptr);
+    const int64_t ld = M->gram_stride;
+    const int h = lane >> 5, col = lane & 31;
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < 2; ++y) {
+            const int ib = ti * kGramTile + wm * 64 + x * 32;
+            const int64_t j = tj * kGramTile + wn * 64 + y * 32 + col;
+            if (j >= channels) continue;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int64_t i0 = ib + 8 * g + 4 * h;  // rows i0 .. i0 + 3 (channels % 8 == 0: all or none in range)
+                if (i0 >= channels) continue;
+                if (!diagonal) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) G[(i0 + r) * ld + j] = acc[x][y][4 * g + r];
+                    // Mirror: G[j][i0 .. i0 + 3] is one 16-byte store.
+                    const f4 v = {acc[x][y][4 * g], acc[x][y][4 * g + 1], acc[x][y][4 * g + 2], acc[x][y][4 * g + 3]};
+                    *reinterpret_cast<RCH_GLOBAL f4*>(G + j * ld + i0) = v;
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int64_t i = i0 + r;
+                        if (i >= j) {  // lower triangle, mirrored
+                            G[i * ld + j] = acc[x][y][4 * g + r];
+                            G[j * ld + i] = acc[x][y][4 * g + r];
+                        }
+                    }
+                }
+            }
+        }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Projection P = X Q^T on v_mfma_f64_16x16x4f64: D[m = token][n = rank] = sum_c X[token][c] Q[rank][c].
+// Workgroup (64-token tile, 64-rank chunk, matrix); wave w owns tokens 16w .. 16w + 15 of the
+// tile and the chunk's 4 rank blocks of 16.  Per 32-channel step a lane (i = l % 16, group
+// g = l / 16) loads channels 8g .. 8g + 7 of its token row and of its basis row (16-byte loads,
+// no LDS), and MFMA step s takes channel 8g + s from every group.  The f64 accumulator holds
+// element v of lane l at row (l / 16) + 4v, column l % 16: token g + 4v, rank i of the block.
+// ---------------------------------------------------------------------------------------------
+
+template <int DT>
+__global__ void __launch_bounds__(kThreads) project_kernel(const rch_fit_matrix* __restrict__ mats, int channels) {
+    const rch_fit_matrix* M = mats + blockIdx.z;
+    const int64_t rows = M->rows;
+    const int rank = static_cast<int>(M->rank);
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 64;
+    const int r0 = blockIdx.y * 64;
+    if (t0 >= rows || r0 >= rank) return;
+    constexpr int E = esize<DT>();
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int g = lane >> 4, i16 = lane & 15;
+    const int64_t wt = t0 + 16 * wave;  // first token of this wave
+    const __amdgpu_buffer_rsrc_t xs = source_rows<DT>(M, channels, wt);
+    const __amdgpu_buffer_rsrc_t qs = make_rsrc(M->basis_ptr, ((rank - 1) * M->basis_stride + channels) * 2);
+    const uint32_t x_row = static_cast<uint32_t>(i16 * M->src_stride * E);
+
+    d4 acc[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) acc[b] = d4{};
+    for (int c0 = 0; c0 < channels; c0 += 32) {
+        const int c = c0 + 8 * g;
+        double xv[8];
+        load8<DT>(xs, c < channels ? x_row + static_cast<uint32_t>(c * E) : kOutOfRange, xv);
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int k = r0 + 16 * b + i16;
+            const uint32_t q_off =
+                (k < rank && c < channels) ? static_cast<uint32_t>((k * M->basis_stride + c) * 2) : kOutOfRange;
+            double qv[8];
+            load8<RCH_DT_F16>(qs, q_off, qv);
+#pragma unroll
+            for (int s = 0; s < 8; ++s) acc[b] = __builtin_amdgcn_mfma_f64_16x16x4f64(xv[s], qv[s], acc[b], 0, 0, 0);
+        }
+    }
+
+    RCH_GLOBAL float* out = gout<float>(M->coef_ptr);
+    unsigned int* ext = reinterpret_cast<unsigned int*>(M->extrema_ptr);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const int k = r0 + 16 * b + i16;  // this lane's rank
+        uint32_t lo = 0u, hi = 0u;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int64_t t = wt + g + 4 * v;
+            const float value = static_cast<float>(acc[b][v]);
+            if (t < rows) {
+                if (k < rank) out[t * M->coef_stride + k] = value;  // 16 lanes: 64 contiguous bytes of a row
+                const uint32_t key = order_key(value);
+                lo = ~key > lo ? ~key : lo;
+                hi = key > hi ? key : hi;
+            }
+        }
+        if (ext) {
+#pragma unroll
+            for (int d = 16; d <= 32; d <<= 1) {  // over the 4 token groups
+                const uint32_t ol = __shfl_xor(lo, d), oh = __shfl_xor(hi, d);
+                lo = ol > lo ? ol : lo;
+                hi = oh > hi ? oh : hi;
+            }
+            if (g == 0 && k < rank) {
+                atomicMax(ext + k, lo);  // vector atomics
+                atomicMax(ext + rank + k, hi);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Residual energies on v_mfma_f64_16x16x4f64: D[m = channel][n = token] = sum_k Q[k][c] P[token][k].
+// Workgroup = 64-token tile of one matrix, wave w = tokens 16w .. 16w + 15, looping over
+// 16-channel blocks.  Per 16-rank step a lane (i = l % 16, g = l / 16) loads P[token i][4g .. 4g + 3]
+// (one 16-byte load) and Q[4g .. 4g + 3][channel i]; MFMA step j takes rank 4g + j.
+// The f64 accumulator holds element v of lane l at row (l / 16) + 4v, column l % 16: channel
+// g + 4v of the block and token i, compared with X[token][channel].
+// ---------------------------------------------------------------------------------------------
+
+template <int DT>
+__global__ void __launch_bounds__(kThreads) residual_kernel(const rch_fit_matrix* __restrict__ mats, int channels) {
+    const rch_fit_matrix* M = mats + blockIdx.y;
+    const int64_t rows = M->rows;
+    const int rank = static_cast<int>(M->rank);
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 64;
+    if (t0 >= rows) return;
+    constexpr int E = esize<DT>();
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int g = lane >> 4, i16 = lane & 15;
+    const int64_t wt = t0 + 16 * wave;
+    const int64_t left = rows - wt;
+    const __amdgpu_buffer_rsrc_t xs = source_rows<DT>(M, channels, wt);
+    const __amdgpu_buffer_rsrc_t ps = make_rsrc(M->coef_ptr + wt * M->coef_stride * 4,
+                                                (rank > 0 && left > 0) ? ((left - 1) * M->coef_stride + rank) * 4 : 0);
+    const __amdgpu_buffer_rsrc_t qs = make_rsrc(M->basis_ptr, rank > 0 ? ((rank - 1) * M->basis_stride + channels) * 2 : 0);
+    const float smax = __uint_as_float(*gin<unsigned int>(M->absmax_ptr));
+    const double s = static_cast<double>(smax);
+    const bool scaled = smax != 0.0f;
+    const uint32_t x_row = static_cast<uint32_t>(i16 * M->src_stride * E);
+    const uint32_t p_row = static_cast<uint32_t>(i16 * M->coef_stride * 4);
+
+    double src = 0.0, err = 0.0;
+    for (int cb = 0; cb < channels; cb += 16) {
+        d4 acc = d4{};
+        for (int k0 = 0; k0 < rank; k0 += 16) {
+            const int k = k0 + 4 * g;
+            const u4 pw = __builtin_amdgcn_raw_buffer_load_b128(ps, k < rank ? p_row + static_cast<uint32_t>(k * 4) : kOutOfRange,
+                                                                0, 0);
+            double qa[4], pb[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bool in = k + j < rank;  // P rows may hold padding beyond the rank
+                pb[j] = in ? static_cast<double>(__uint_as_float(pw[j])) : 0.0;
+                const uint32_t q_off = (in && cb + i16 < channels)
+                                           ? static_cast<uint32_t>(((k + j) * M->basis_stride + cb + i16) * 2)
+                                           : kOutOfRange;
+                const uint32_t qb = __builtin_amdgcn_raw_buffer_load_b16(qs, q_off, 0, 0);
+                qa[j] = static_cast<double>(half_bits<RCH_DT_F16>(qb));
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f64_16x16x4f64(qa[j], pb[j], acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int c = cb + g + 4 * v;
+            const uint32_t offset = c < channels ? x_row + static_cast<uint32_t>(c * E) : kOutOfRange;
+            double a;
+            if constexpr (DT == RCH_DT_F32)
+                a = static_cast<double>(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xs, offset, 0, 0)));
+            else
+                a = static_cast<double>(half_bits<DT>(__builtin_amdgcn_raw_buffer_load_b16(xs, offset, 0, 0)));
+            double e = a - acc[v];
+            if (scaled) {
+                a = a / s;
+                e = e / s;
+            }
+            src += a * a;
+            err += e * e;
+        }
+    }
+    // Fixed-order reduction: butterfly within the wave, then waves 0..3 in order.
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        src += __shfl_xor(src, d);
+        err += __shfl_xor(err, d);
+    }
+    __shared__ double part[2][kThreads / 64];
+    if (lane == 0) {
+        part[0][wave] = src;
+        part[1][wave] = err;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double a = 0.0, b = 0.0;
+        for (int w = 0; w < kThreads / 64; ++w) {
+            a += part[0][w];
+            b += part[1][w];
+        }
+        RCH_GLOBAL double* out = gout<double>(M->partial_ptr) + 2 * blockIdx.x;
+        out[0] = a;
+        out[1] = b;
+    }
+}
+
+// Sum of the per-tile partials of each matrix in tile order (one workgroup per matrix).
+__global__ void __launch_bounds__(64) energy_total_kernel(const rch_fit_matrix* __restrict__ mats) {
+    const rch_fit_matrix* M = mats + blockIdx.x;
+    if (threadIdx.x != 0) return;
+    const int64_t tiles = (M->rows + 63) / 64;
+    const RCH_GLOBAL double* p = gin<double>(M->partial_ptr);
+    double a = 0.0, b = 0.0;
+    for (int64_t t = 0; t < tiles; ++t) {
+        a += p[2 * t];
+        b += p[2 * t + 1];
+    }
+    RCH_GLOBAL double* out = gout<double>(M->energy_ptr);
+    out[0] = a;
+    out[1] = b;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Column extrema and the FP64 quantizer of an fp32 [rows, cols] matrix: workgroup = 64 rows,
+// threads stride over the columns (consecutive threads, consecutive columns).
+// ---------------------------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(kThreads) extrema_kernel(const float* __restrict__ values, int64_t rows, int cols,
+                                                           int64_t stride, unsigned int* __restrict__ keys) {
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * 64;
+    const int64_t r1 = rows - r0 < 64 ? rows : r0 + 64;
+    for (int c = threadIdx.x; c < cols; c += kThreads) {
+        uint32_t lo = 0u, hi = 0u;
+        for (int64_t r = r0; r < r1; ++r) {
+            const uint32_t k = order_key(values[r * stride + c]);
+            lo = ~k > lo ? ~k : lo;
+            hi = k > hi ? k : hi;
+        }
+        atomicMax(keys + c, lo);  // vector atomics
+        atomicMax(keys + cols + c, hi);
+    }
+}
+
+__global__ void __launch_bounds__(kThreads) quantize_kernel(const float* __restrict__ values, int64_t rows, int cols,
+                                                            int64_t stride, const double* __restrict__ scale,
+                                                            const double* __restrict__ offset,
+                                                            uint8_t* __restrict__ codes, int64_t code_stride) {
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * 64;
+    const int64_t r1 = rows - r0 < 64 ? rows : r0 + 64;
+    for (int c = threadIdx.x; c < cols; c += kThreads) {
+        const double sc = scale[c], of = offset[c];
+        for (int64_t r = r0; r < r1; ++r) {
+            double q = 0.0;
+            if (sc > 0.0) q = rint((static_cast<double>(values[r * stride + c]) - of) / sc);
+            q = q < 0.0 ? 0.0 : (q > 255.0 ? 255.0 : q);
+            codes[r * code_stride + c] = static_cast<uint8_t>(q);
+        }
+    }
+}
+
+int check_matrices(const rch_fit_matrix* mats, int n, int channels, const char* what) {
+    if (!mats || n <= 0 || n > 65535) return fail(RCH_E_CONFIG, "%s: 1 <= n_mats <= 65535 required", what);
+    if (channels <= 0 || channels % 8 != 0 || channels > (1 << 20))
+        return fail(RCH_E_CONFIG, "%s: channels must be a positive multiple of 8", what);
+    return RCH_OK;
+}
+
+}  // namespace
+}  // namespace rch
+
+using namespace rch;
+
+#define RCH_DISPATCH_DTYPE(dtype, what, KERNEL, GRID, ...)                                                          \
+    switch (dtype) {                                                                                                \
+        case RCH_DT_BF16: hipLaunchKernelGGL(KERNEL<RCH_DT_BF16>, GRID, dim3(kThreads), 0, s, __VA_ARGS__); break; \
+        case RCH_DT_F16: hipLaunchKernelGGL(KERNEL<RCH_DT_F16>, GRID, dim3(kThreads), 0, s, __VA_ARGS__); break;   \
+        case RCH_DT_F32: hipLaunchKernelGGL(KERNEL<RCH_DT_F32>, GRID, dim3(kThreads), 0, s, __VA_ARGS__); break;   \
+        default: return fail(RCH_E_CONFIG, "%s: source dtype must be bf16, f16 or f32", what);                      \
+    }
+
+extern "C" {
+
+int rch_fit_matrix_size(void) { return static_cast<int>(sizeof(rch_fit_matrix)); }
+
+int rch_fit_absmax(const rch_fit_matrix* mats_dev, int n_mats, int channels, int64_t max_rows, int src_dtype,
+                   void* stream) {
+    if (int status = check_matrices(mats_dev, n_mats, channels, "rch_fit_absmax")) return status;
+    if (max_rows <= 0 || (max_rows + 63) / 64 > 0x7fffffff) return fail(RCH_E_CONFIG, "rch_fit_absmax: invalid max_rows");
+    const dim3 grid(static_cast<unsigned>((max_rows + 63) / 64), static_cast<unsigned>(n_mats));
+    hipStream_t s = as_stream(stream);
+    RCH_DISPATCH_DTYPE(src_dtype, "rch_fit_absmax", absmax_kernel, grid, mats_dev, channels);
+    return check_launch("rch_fit_absmax");
+}
+
+int rch_fit_gram(const rch_fit_matrix* mats_dev, int n_mats, int channels, int src_dtype, void* stream) {
+    if (int status = check_matrices(mats_dev, n_mats, channels, "rch_fit_gram")) return status;
+    const int t = (channels + kGramTile - 1) / kGramTile;
+    const int64_t tiles = static_cast<int64_t>(t) * (t + 1) / 2;
+    if (tiles * n_mats > 0x7fffffff) return fail(RCH_E_CONFIG, "rch_fit_gram: too many tiles");
+    const int grid = static_cast<int>(tiles * n_mats);
+    hipStream_t s = as_stream(stream);
+    RCH_DISPATCH_DTYPE(src_dtype, "rch_fit_gram", gram_kernel, dim3(grid), mats_dev, channels, static_cast<int>(tiles),
+                       grid);
+    return check_launch("rch_fit_gram");
+}
+
+int rch_fit_project(const rch_fit_matrix* mats_dev, int n_mats, int channels, int64_t max_rows, int max_rank,
+                    int src_dtype, void* stream) {
+    if (int status = check_matrices(mats_dev, n_mats, channels, "rch_fit_project")) return status;
+    if (max_rows <= 0 || max_rank <= 0 || (max_rows + 63) / 64 > 0x7fffffff || max_rank > channels)
+        return fail(RCH_E_CONFIG, "rch_fit_project: invalid max_rows / max_rank");
+    const dim3 grid(static_cast<unsigned>((max_rows + 63) / 64), static_cast<unsigned>((max_rank + 63) / 64),
+                    static_cast<unsigned>(n_mats));
+    hipStream_t s = as_stream(stream);
+    RCH_DISPATCH_DTYPE(src_dtype, "rch_fit_project", project_kernel, grid, mats_dev, channels);
+    return check_launch("rch_fit_project");
+}
+
+int rch_fit_residual(const rch_fit_matrix* mats_dev, int n_mats, int channels, int64_t max_rows, int src_dtype,
+                     void* stream) {
+    if (int status = check_matrices(mats_dev, n_mats, channels, "rch_fit_residual")) return status;
+    if (max_rows <= 0 || (max_rows + 63) / 64 > 0x7fffffff) return fail(RCH_E_CONFIG, "rch_fit_residual: invalid max_rows");
+    const dim3 grid(static_cast<unsigned>((max_rows + 63) / 64), static_cast<unsigned>(n_mats));
+    hipStream_t s = as_stream(stream);
+    RCH_DISPATCH_DTYPE(src_dtype, "rch_fit_residual", residual_kernel, grid, mats_dev, channels);
+    if (int status = check_launch("rch_fit_residual")) return status;
+    hipLaunchKernelGGL(energy_total_kernel, dim3(n_mats), dim3(64), 0, s, mats_dev);
+    return check_launch("rch_fit_residual (totals)");
+}
+
+int rch_column_extrema(const float* values_dev, int64_t rows, int cols, int64_t stride, uint32_t* keys_dev,
+                       void* stream) {
+    if (!values_dev || !keys_dev || rows <= 0 || cols <= 0 || stride < cols || (rows + 63) / 64 > 0x7fffffff)
+        return fail(RCH_E_CONFIG, "rch_column_extrema: invalid arguments");
+    hipLaunchKernelGGL(extrema_kernel, dim3(static_cast<unsigned>((rows + 63) / 64)), dim3(kThreads), 0,
+                       as_stream(stream), values_dev, rows, cols, stride, reinterpret_cast<unsigned int*>(keys_dev));
+    return check_launch("rch_column_extrema");
+}
+
+int rch_quantize(const float* values_dev, int64_t rows, int cols, int64_t stride, const double* scale_dev,
+                 const double* offset_dev, uint8_t* codes_dev, int64_t code_stride, void* stream) {
+    if (!values_dev || !scale_dev || !offset_dev || !codes_dev || rows <= 0 || cols <= 0 || stride < cols ||
+        code_stride < cols || (rows + 63) / 64 > 0x7fffffff)
+        return fail(RCH_E_CONFIG, "rch_quantize: invalid arguments");
+    hipLaunchKernelGGL(quantize_kernel, dim3(static_cast<unsigned>((rows + 63) / 64)), dim3(kThreads), 0,
+                       as_stream(stream), values_dev, rows, cols, stride, scale_dev, offset_dev, codes_dev, code_stride);
+    return check_launch("rch_quantize");
+}
+
+}  // extern "C"

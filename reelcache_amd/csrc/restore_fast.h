@@ -24,14 +24,6 @@
 namespace rch {
 namespace {
 
-constexpr int kBufferWord3 = 0x00020000;  // raw buffer resource word 3 for the gfx9 family
-constexpr uint32_t kOutOfRange = 0x80000000u;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(int64_t base, int64_t bytes) {
-    const int records = bytes > 0x7fffffff ? 0x7fffffff : static_cast<int>(bytes < 0 ? 0 : bytes);
-    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(base), 0, records, kBufferWord3);
-}
-
 struct Cursor {
     int tile, bp, head;
 };

@@ -26,32 +26,12 @@
 //     buffered, and shared by the 4 waves.
 #include "common.h"
 
-#define RCH_GLOBAL __attribute__((address_space(1)))
-
 namespace rch {
 namespace {
-
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
-typedef float f16v __attribute__((ext_vector_type(16)));
-typedef float f4 __attribute__((ext_vector_type(4)));
-typedef unsigned int u4 __attribute__((ext_vector_type(4)));  // native vectors: promotable to registers
-typedef unsigned int u2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kTileTokens = 32 * kWaves;
-
-// Device addresses arrive as int64 descriptor fields; these views make the compiler emit
-// global (not flat) memory instructions.
-template <typename T>
-__device__ __forceinline__ const RCH_GLOBAL T* gin(int64_t address) {
-    return reinterpret_cast<const RCH_GLOBAL T*>(address);
-}
-template <typename T>
-__device__ __forceinline__ RCH_GLOBAL T* gout(int64_t address) {
-    return reinterpret_cast<RCH_GLOBAL T*>(address);
-}
 
 // Channel held by MFMA row m of a 32-channel block.  Lane half h of a 32x32 accumulator
 // holds rows {8g + 4h + r}; mapping them to 16h + 4g + r puts 16 consecutive channels,

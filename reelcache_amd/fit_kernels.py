@@ -1,0 +1,250 @@
+"""Host side of the fit kernels (``rch_fit_*``, ``rch_column_extrema``, ``rch_quantize``).
+
+Each function builds the ``rch_fit_matrix`` descriptor table of a batch, allocates the device
+outputs (torch is used for memory and streams only) and launches on the current stream of the
+sources' device.  Every result stays on the device; callers read what they need once.  CPU
+tensors and a missing library raise :class:`UnsupportedError` -- there is no host fallback.
+
+Layout rules the kernels rely on (violating inputs are copied into zero-padded buffers here):
+rows of X and Q start 16-byte aligned with unit column stride, and channels % 8 == 0.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import _lib
+from .errors import ConfigurationError, UnsupportedError
+
+_DTYPE_CODES = {torch.bfloat16: _lib.DT_BF16, torch.float16: _lib.DT_F16, torch.float32: _lib.DT_F32}
+#: fp32 bits of +inf: an absmax key at or above it marks a non-finite source element.
+NONFINITE_BITS = 0x7F800000
+_ROW_TILE = 64  # rows per partial energy
+
+
+def _device(tensors) -> torch.device:
+    devices = {tensor.device for tensor in tensors}
+    if len(devices) != 1:
+        raise ConfigurationError("one fit batch must live on one device")
+    (device,) = devices
+    if device.type != "cuda":
+        raise UnsupportedError("the fit kernels run on the GPU (HIP, gfx950); move the matrices to a cuda device")
+    _lib.library()  # raises UnsupportedError with the reason when the library is unavailable
+    return device
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def padded(channels: int) -> int:
+    return -(-channels // 8) * 8
+
+
+def _aligned(x: torch.Tensor, channels: int) -> torch.Tensor:
+    """``x`` when the kernels can read it in place, else a copy into a zero-padded buffer."""
+    size = x.element_size()
+    if (x.shape[1] == channels and x.stride(1) == 1 and x.stride(0) >= channels
+            and (x.stride(0) * size) % 16 == 0 and x.data_ptr() % 16 == 0):
+        return x
+    out = torch.zeros((x.shape[0], channels), dtype=x.dtype, device=x.device)
+    out[:, :x.shape[1]].copy_(x)
+    return out
+
+
+def _check_sources(sources) -> tuple[list[torch.Tensor], int, int]:
+    if not sources:
+        raise ConfigurationError("a fit batch needs at least one matrix")
+    channels = {int(x.shape[1]) for x in sources}
+    if len(channels) != 1:
+        raise ConfigurationError("one fit batch must share the channel count")
+    dtypes = {x.dtype for x in sources}
+    if len(dtypes) != 1 or next(iter(dtypes)) not in _DTYPE_CODES:
+        raise UnsupportedError("the fit kernels take one of bfloat16, float16 or float32 per batch")
+    for x in sources:
+        if x.ndim != 2 or x.shape[0] < 1 or x.shape[1] < 1:
+            raise ConfigurationError("fit sources must be nonempty 2-D matrices")
+    (c,) = channels
+    c8 = padded(c)
+    return [_aligned(x, c8) for x in sources], c, c8
+
+
+def _table(count: int) -> np.ndarray:
+    return np.zeros(count, dtype=_lib.FIT_DTYPE)
+
+
+def _upload(table: np.ndarray, device: torch.device) -> torch.Tensor:
+    return torch.from_numpy(table.view(np.int64).copy()).to(device)
+
+
+def _fill_sources(table: np.ndarray, sources) -> None:
+    for row, x in zip(table, sources):
+        row["src_ptr"] = x.data_ptr()
+        row["src_dtype"] = _DTYPE_CODES[x.dtype]
+        row["rows"] = x.shape[0]
+        row["src_stride"] = x.stride(0)
+
+
+def decode_max_keys(keys) -> np.ndarray:
+    """fp32 values of order-preserving keys (the per-column maxima)."""
+    k = np.asarray(keys, dtype=np.int64).astype(np.uint32)
+    bits = np.where(k & np.uint32(0x80000000), k & np.uint32(0x7FFFFFFF), ~k)
+    return bits.astype(np.uint32).view(np.float32)
+
+
+def decode_min_keys(keys) -> np.ndarray:
+    """fp32 values of inverted order-preserving keys (the per-column minima)."""
+    return decode_max_keys(~np.asarray(keys, dtype=np.int64).astype(np.uint32))
+
+
+# ---------------------------------------------------------------------------------------------
+# Batched entry points
+# ---------------------------------------------------------------------------------------------
+
+
+def absmax(sources) -> torch.Tensor:
+    """int32 [n]: fp32 bits of max|X| of each source (>= NONFINITE_BITS when X holds inf/nan)."""
+    device = _device(sources)
+    aligned, _, c8 = _check_sources(sources)
+    keys = torch.zeros(len(aligned), dtype=torch.int32, device=device)
+    table = _table(len(aligned))
+    _fill_sources(table, aligned)
+    table["absmax_ptr"] = keys.data_ptr() + 4 * np.arange(len(aligned))
+    descriptors = _upload(table, device)
+    max_rows = max(int(x.shape[0]) for x in aligned)
+    _lib.call("rch_fit_absmax", descriptors.data_ptr(), len(aligned), c8, max_rows, _DTYPE_CODES[aligned[0].dtype],
+              _stream(device))
+    return keys
+
+
+def gram(sources) -> torch.Tensor:
+    """fp32 [n, C, C]: exactly symmetric X^T X of each source (MFMA, exact products)."""
+    device = _device(sources)
+    aligned, channels, c8 = _check_sources(sources)
+    grams = torch.empty((len(aligned), c8, c8), dtype=torch.float32, device=device)
+    table = _table(len(aligned))
+    _fill_sources(table, aligned)
+    table["gram_ptr"] = grams.data_ptr() + 4 * c8 * c8 * np.arange(len(aligned))
+    table["gram_stride"] = c8
+    descriptors = _upload(table, device)
+    _lib.call("rch_fit_gram", descriptors.data_ptr(), len(aligned), c8, _DTYPE_CODES[aligned[0].dtype], _stream(device))
+    return grams if c8 == channels else grams[:, :channels, :channels]
+
+
+def _aligned_basis(basis: torch.Tensor, rank: int, c8: int) -> torch.Tensor:
+    if basis.dtype != torch.float16:
+        raise ConfigurationError("the stored basis must be float16")
+    view = basis[:rank]
+    return _aligned(view, c8)
+
+
+def project(sources, bases, ranks, *, extrema: bool = False):
+    """``(coefficients, keys)``: fp32 P = X Q[:rank]^T per source (FP64-accumulated MFMA) and,
+    with ``extrema``, int32 [n, 2 * max_rank] order keys of the columns of P: row i holds
+    ~key(min) of its columns in [0, rank_i) and key(max) in [rank_i, 2 rank_i) (see :func:`split_keys`)."""
+    device = _device(sources)
+    aligned, _, c8 = _check_sources(sources)
+    if len(bases) != len(aligned) or len(ranks) != len(aligned):
+        raise ConfigurationError("projection needs one basis and one rank per source")
+    table = _table(len(aligned))
+    _fill_sources(table, aligned)
+    keep, outputs = [], []
+    max_rank = max(int(r) for r in ranks)
+    keys = torch.zeros((len(aligned), 2 * max_rank), dtype=torch.int32, device=device) if extrema else None
+    for index, (x, basis, rank) in enumerate(zip(aligned, bases, ranks)):
+        rank = int(rank)
+        if not 1 <= rank <= basis.shape[0] or basis.shape[1] > c8 or basis.device != device:
+            raise ConfigurationError("projection basis does not match its source")
+        q = _aligned_basis(basis, rank, c8)
+        stride = -(-rank // 4) * 4
+        p = torch.empty((x.shape[0], stride), dtype=torch.float32, device=device)
+        keep.append(q)
+        outputs.append(p[:, :rank])
+        row = table[index]
+        row["basis_ptr"], row["basis_stride"], row["rank"] = q.data_ptr(), q.stride(0), rank
+        row["coef_ptr"], row["coef_stride"] = p.data_ptr(), stride
+        if extrema:
+            row["extrema_ptr"] = keys[index].data_ptr()
+    descriptors = _upload(table, device)
+    max_rows = max(int(x.shape[0]) for x in aligned)
+    _lib.call("rch_fit_project", descriptors.data_ptr(), len(aligned), c8, max_rows, max_rank,
+              _DTYPE_CODES[aligned[0].dtype], _stream(device))
+    del keep
+    return outputs, keys
+
+
+def split_keys(keys_row, rank: int) -> tuple[np.ndarray, np.ndarray]:
+    """Host fp32 (min, max) of each of the ``rank`` columns from one row of :func:`project` keys."""
+    row = np.asarray(keys_row)
+    return decode_min_keys(row[:rank]), decode_max_keys(row[rank:2 * rank])
+
+
+def energies(sources, absmax_keys: torch.Tensor, *, bases=None, ranks=None, coefficients=None) -> torch.Tensor:
+    """float64 [n, 2]: sum (X/s)^2 and sum ((X - P Q)/s)^2 per source, s = max|X| from ``absmax_keys``
+    (FP64, fixed-order sums); without bases only the source energy (second column = first)."""
+    device = _device(sources)
+    aligned, _, c8 = _check_sources(sources)
+    n = len(aligned)
+    if absmax_keys.shape != (n,) or absmax_keys.dtype != torch.int32 or absmax_keys.device != device:
+        raise ConfigurationError("energies need the int32 absmax keys of the same batch")
+    with_basis = bases is not None
+    if with_basis and not (len(bases) == len(ranks) == len(coefficients) == n):
+        raise ConfigurationError("residual energies need one basis, rank and coefficient matrix per source")
+    table = _table(n)
+    _fill_sources(table, aligned)
+    tiles = [-(-int(x.shape[0]) // _ROW_TILE) for x in aligned]
+    partials = torch.empty(2 * sum(tiles), dtype=torch.float64, device=device)
+    totals = torch.empty((n, 2), dtype=torch.float64, device=device)
+    table["absmax_ptr"] = absmax_keys.data_ptr() + 4 * np.arange(n)
+    table["energy_ptr"] = totals.data_ptr() + 16 * np.arange(n)
+    table["partial_ptr"] = partials.data_ptr() + 16 * np.concatenate(([0], np.cumsum(tiles)[:-1]))
+    keep = []
+    if with_basis:
+        for index, (x, basis, rank, p) in enumerate(zip(aligned, bases, ranks, coefficients)):
+            rank = int(rank)
+            if not 1 <= rank <= basis.shape[0] or p.shape != (x.shape[0], rank) or p.dtype != torch.float32:
+                raise ConfigurationError("residual coefficients do not match their source and rank")
+            q = _aligned_basis(basis, rank, c8)
+            if p.stride(1) != 1 or (p.stride(0) * 4) % 16 or p.data_ptr() % 16:
+                stride = -(-rank // 4) * 4
+                copy = torch.zeros((p.shape[0], stride), dtype=torch.float32, device=device)
+                copy[:, :rank].copy_(p)
+                p = copy
+            keep += [q, p]
+            row = table[index]
+            row["basis_ptr"], row["basis_stride"], row["rank"] = q.data_ptr(), q.stride(0), rank
+            row["coef_ptr"], row["coef_stride"] = p.data_ptr(), p.stride(0)
+    descriptors = _upload(table, device)
+    _lib.call("rch_fit_residual", descriptors.data_ptr(), n, c8, max(int(x.shape[0]) for x in aligned),
+              _DTYPE_CODES[aligned[0].dtype], _stream(device))
+    del keep
+    return totals
+
+
+def column_extrema(values: torch.Tensor) -> torch.Tensor:
+    """int32 [2 * cols] order keys of every column of an fp32 matrix: ~key(min) then key(max)
+    (the layout :func:`split_keys` reads with ``rank = cols``)."""
+    device = _device([values])
+    if values.dtype != torch.float32 or values.ndim != 2 or min(values.shape) < 1 or values.stride(1) != 1:
+        raise ConfigurationError("column extrema take a nonempty fp32 matrix with unit column stride")
+    keys = torch.zeros(2 * values.shape[1], dtype=torch.int32, device=device)
+    _lib.call("rch_column_extrema", values.data_ptr(), values.shape[0], values.shape[1], values.stride(0),
+              keys.data_ptr(), _stream(device))
+    return keys
+
+
+def quantize(values: torch.Tensor, scale: torch.Tensor, offset: torch.Tensor) -> torch.Tensor:
+    """uint8 codes clamp(rint((v - offset) / scale), 0, 255) in FP64 (0 where scale == 0)."""
+    device = _device([values])
+    if values.dtype != torch.float32 or values.ndim != 2 or min(values.shape) < 1 or values.stride(1) != 1:
+        raise ConfigurationError("quantization takes a nonempty fp32 matrix with unit column stride")
+    cols = values.shape[1]
+    for vector in (scale, offset):
+        if vector.dtype != torch.float64 or vector.shape != (cols,) or vector.device != device:
+            raise ConfigurationError("quantization needs float64 scale and offset vectors per column")
+    scale, offset = scale.contiguous(), offset.contiguous()
+    codes = torch.empty(values.shape, dtype=torch.uint8, device=device)
+    _lib.call("rch_quantize", values.data_ptr(), values.shape[0], cols, values.stride(0), scale.data_ptr(),
+              offset.data_ptr(), codes.data_ptr(), codes.stride(0), _stream(device))
+    return codes

@@ -1,0 +1,162 @@
+"""GPU parity of the fit kernels (through the C ABI) against the FP64 oracle.
+
+* absmax: exact; non-finite sources flagged.
+* Gram: exactly symmetric; within the fp32 summation bound of the FP64 Gram of the exact values.
+* projection: the fp32 rounding of the FP64 dot product -- equal to the oracle except for
+  elements within ~1e-13 relative of an fp32 rounding boundary (at most one ulp); the fused
+  per-column extrema are exactly the min / max of the returned coefficients.
+* energies: FP64, relative 1e-12 of the oracle.
+* quantizer: codes bit-exact with the oracle on the same coefficients and affine.
+"""
+
+import functools
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fit as of
+from oracle import quantize as oq
+from reelcache_amd import fit_kernels as fk
+from reelcache_amd import quantize as pq
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = {"bfloat16": torch.bfloat16, "float16": torch.float16, "float32": torch.float32}
+
+
+def _source(rng, rows, channels, dtype, device, spectrum=False):
+    if spectrum:
+        x = of.decaying_spectrum(rng, rows, channels)
+    else:
+        x = (rng.standard_normal((rows, channels)) * rng.lognormal(0, 1, channels)).astype(np.float32)
+    tensor = torch.from_numpy(x).to(DTYPES[dtype]).to(device)
+    return tensor, tensor.float().cpu().numpy()
+
+
+def _basis(rng, rank, channels, device):
+    q, _ = np.linalg.qr(rng.standard_normal((channels, rank)))
+    basis = of.stored_basis(q.T)
+    return torch.from_numpy(basis).to(device), basis
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
+def test_absmax_exact_and_nonfinite(device, dtype):
+    rng = np.random.default_rng(10)
+    a, a_host = _source(rng, 300, 136, dtype, device)
+    b, b_host = _source(rng, 65, 136, dtype, device)
+    c, _ = _source(rng, 64, 136, dtype, device)
+    c[17, 99] = float("inf")
+    keys = fk.absmax([a, b, c]).cpu().numpy().astype(np.uint32)
+    assert keys[0].view(np.float32) == np.abs(a_host).max()
+    assert keys[1].view(np.float32) == np.abs(b_host).max()
+    assert keys[2] >= fk.NONFINITE_BITS
+
+
+@pytest.mark.parametrize("dtype,rows,channels", [("bfloat16", 300, 136), ("float16", 257, 256),
+                                                 ("float32", 129, 200), ("bfloat16", 4680, 1536)])
+def test_gram_symmetric_and_within_fp32_bound(device, dtype, rows, channels):
+    rng = np.random.default_rng(11)
+    sources, hosts = zip(*[_source(rng, rows - 7 * i, channels, dtype, device) for i in range(2)])
+    grams = fk.gram(list(sources)).cpu().numpy()
+    for gram, host in zip(grams, hosts):
+        np.testing.assert_array_equal(gram, gram.T)  # exactly symmetric
+        expected = of.gram(host)
+        bound = (host.shape[0] + 2) * 2.0 ** -24 * (np.abs(host).T.astype(np.float64) @ np.abs(host))
+        assert np.all(np.abs(gram - expected) <= bound + 1e-30)
+
+
+def test_gram_pads_unaligned_channels(device):
+    rng = np.random.default_rng(12)
+    x, host = _source(rng, 50, 13, "float32", device)
+    gram = fk.gram([x]).cpu().numpy()
+    assert gram.shape == (1, 13, 13)
+    np.testing.assert_allclose(gram[0], of.gram(host), rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("dtype,rows,channels,rank", [("bfloat16", 300, 136, 40), ("float16", 129, 256, 64),
+                                                      ("float32", 100, 64, 7), ("bfloat16", 4680, 1536, 128)])
+def test_projection_rounds_the_fp64_product(device, dtype, rows, channels, rank):
+    rng = np.random.default_rng(13)
+    x, host = _source(rng, rows, channels, dtype, device)
+    q, q_host = _basis(rng, rank + 3, channels, device)
+    (p,), keys = fk.project([x], [q], [rank], extrema=True)
+    p = p.cpu().numpy()
+    expected = of.project(host, q_host, rank)
+    differ = p != expected
+    assert differ.mean() <= 1e-4
+    if differ.any():
+        ulp = np.abs(p[differ].view(np.int32).astype(np.int64) - expected[differ].view(np.int32).astype(np.int64))
+        assert ulp.max() <= 1
+    low, high = fk.split_keys(keys[0].cpu().numpy(), rank)
+    np.testing.assert_array_equal(low, p.min(0))
+    np.testing.assert_array_equal(high, p.max(0))
+
+
+def test_projection_batch_of_ragged_ranks(device):
+    rng = np.random.default_rng(14)
+    xs, hosts, qs, q_hosts = [], [], [], []
+    ranks = [5, 32, 61]
+    for i, rank in enumerate(ranks):
+        x, host = _source(rng, 90 + 31 * i, 64, "bfloat16", device)
+        q, q_host = _basis(rng, rank, 64, device)
+        xs.append(x), hosts.append(host), qs.append(q), q_hosts.append(q_host)
+    coefficients, _ = fk.project(xs, qs, ranks)
+    for p, host, q_host, rank in zip(coefficients, hosts, q_hosts, ranks):
+        expected = of.project(host, q_host, rank)
+        assert p.shape == expected.shape
+        assert (p.cpu().numpy() == expected).mean() >= 0.999
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
+def test_energies_match_fp64(device, dtype):
+    rng = np.random.default_rng(15)
+    x, host = _source(rng, 1000, 256, dtype, device, spectrum=True)
+    y, y_host = _source(rng, 77, 256, dtype, device)
+    q, q_host = _basis(rng, 24, 256, device)
+    r, r_host = _basis(rng, 3, 256, device)
+    keys = fk.absmax([x, y])
+    coefficients, _ = fk.project([x, y], [q, r], [24, 3])
+    totals = fk.energies([x, y], keys, bases=[q, r], ranks=[24, 3], coefficients=coefficients).cpu().numpy()
+    for total, host_x, basis, p, rank in zip(totals, (host, y_host), (q_host, r_host), coefficients, (24, 3)):
+        _, source, error = of.energies(host_x, basis, p.cpu().numpy(), rank)
+        assert total[0] == pytest.approx(source, rel=1e-12)
+        assert total[1] == pytest.approx(error, rel=1e-12)
+    source_only = fk.energies([x], fk.absmax([x])).cpu().numpy()
+    assert source_only[0, 0] == pytest.approx(of.energies(host)[1], rel=1e-12)
+
+
+def test_zero_matrix_energies(device):
+    x = torch.zeros((70, 64), dtype=torch.bfloat16, device=device)
+    keys = fk.absmax([x])
+    assert int(keys.cpu()[0]) == 0
+    assert fk.energies([x], keys).cpu().numpy().tolist() == [[0.0, 0.0]]
+
+
+@functools.lru_cache(maxsize=1)
+def _causvid_spectrum():
+    rng = np.random.default_rng(16)
+    return of.decaying_spectrum(rng, 4680, 1536), np.linalg.qr(rng.standard_normal((1536, 32)))[0].T
+
+
+@pytest.mark.parametrize("normalization,fraction", [("per_channel", 1.0), ("global", 0.0), ("leading_columns", 0.25)])
+def test_quantizer_bit_exact(device, normalization, fraction):
+    x_host, rows = _causvid_spectrum()
+    x = torch.from_numpy(x_host).to(torch.bfloat16).to(device)
+    q = torch.from_numpy(of.stored_basis(rows)).to(device)
+    (p,), keys = fk.project([x], [q], [32], extrema=True)
+    values = p.contiguous()
+    layout = pq.normalization_layout(32, normalization, fraction)
+    low, high = fk.split_keys(keys[0].cpu().numpy(), 32)
+    affine = pq.affine_from_extrema(low, high, layout)
+    scale, offset = pq.expanded_affine(affine, layout, 32)
+    codes = fk.quantize(values, torch.from_numpy(np.asarray(scale, np.float64)).to(device),
+                        torch.from_numpy(np.asarray(offset, np.float64)).to(device)).cpu().numpy()
+    host_p = values.cpu().numpy()
+    o_codes, o_affine, _ = oq.quantize(host_p, normalization, fraction)
+    np.testing.assert_array_equal(affine, o_affine)
+    np.testing.assert_array_equal(codes, o_codes)
+    # The standalone extrema kernel agrees with the fused ones.
+    low2, high2 = fk.split_keys(fk.column_extrema(values).cpu().numpy(), 32)
+    np.testing.assert_array_equal(low2, low)
+    np.testing.assert_array_equal(high2, high)
