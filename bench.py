@@ -166,6 +166,149 @@ def cpu_baseline(seconds_budget=20.0, seed=1):
                       f"{elapsed:.1f} s, {elapsed / layers * 1e3:.0f} ms/layer"}
 
 
+# ---------------------------------------------------------------------------------------------
+# Fit leg: one chunk = 30 layers x {K, V} matrices [4680, 1536] bf16 with a
+# decaying spectrum sigma_i = i ** -1.2 plus noise; planned (Gram -> eigh -> crossing -> verified
+# bucket rank), projected onto the planned rows and quantized to uint8 on the device.
+# ---------------------------------------------------------------------------------------------
+
+FIT_EXPONENT, FIT_NOISE = 1.2, 1e-3
+
+
+def fit_workload(device, seed=2, distinct=60):
+    """The chunk's 60 source matrices, generated on the device: X = U diag(sigma) V^T + noise with
+    U, V the Q factors of seeded Gaussians (per matrix) and noise N(0, (1e-3 sigma_1)^2 / N)."""
+    from reelcache_amd.types import MatrixKey, ModelIdentity, TensorContext
+
+    generator = torch.Generator(device=device).manual_seed(seed)
+    sigma = torch.arange(1, CHANNELS + 1, dtype=torch.float32, device=device) ** -FIT_EXPONENT
+    model = ModelIdentity("causvid-synthetic", "c" * 64, LAYERS, CHANNELS, "THD", "bfloat16")
+    sources, contexts = {}, {}
+    for index in range(min(distinct, 2 * LAYERS)):
+        u = torch.linalg.qr(torch.randn(TOKENS, CHANNELS, device=device, generator=generator)).Q
+        v = torch.linalg.qr(torch.randn(CHANNELS, CHANNELS, device=device, generator=generator)).Q
+        noise = torch.randn(TOKENS, CHANNELS, device=device, generator=generator) * (FIT_NOISE / math.sqrt(TOKENS))
+        x = ((u * sigma) @ v.T.contiguous() + noise).to(torch.bfloat16)
+        key = MatrixKey(index // 2, "KV"[index % 2])
+        sources[key] = x
+        contexts[key] = TensorContext(model, key, 0, *GRID, "pre_rope" if key.target == "K" else "none")
+    torch.cuda.synchronize(device)
+    return sources, contexts
+
+
+def fit_step(sources, contexts, device):
+    """One chunk: plan every matrix, then project onto its planned rows and quantize (device)."""
+    from reelcache_amd import fit_kernels as fk
+    from reelcache_amd import gpu_fitting as gf
+    from reelcache_amd import node_packets as npk
+    from reelcache_amd import rank_method as rm
+    from reelcache_amd.types import CodecSpec, energy_targets
+
+    config = rm.RankMethodConfig(energy_targets("causvid"), CodecSpec("svd_hevc", 1))
+    label, solver = gf.select_eigh_solver("auto")
+    keys = list(sources)
+    plan = rm.GramPlanner(config, device=device, eigh=solver, eigh_label=label).plan(
+        sources, contexts, {k: rm.ActiveBasisBinding() for k in keys}, {k: None for k in keys},
+        chunk_id="bench", source_ids={k: str(k) for k in keys})
+    rows = [plan.plans[k].new_rows.to(device) for k in keys]
+    ranks = [int(r.shape[0]) for r in rows]
+    coefficients, extrema = fk.project([sources[k] for k in keys], rows, ranks, extrema=True)
+    host_keys = extrema.cpu().numpy()
+    codes = [npk.quantize_with_extrema(p, host_keys[i], config.spec_for(ranks[i]))[0]
+             for i, p in enumerate(coefficients)]
+    torch.cuda.synchronize(device)
+    return plan, codes
+
+
+def fit_cpu_baseline(seconds_budget=20.0, seed=3):
+    """The oracle's CPU restatement of the fit chain per matrix (FP32 Gram, LAPACK eigh, crossing,
+    FP64-accumulated projection, 8-bit quantization) on a bounded sample of CausVid-shape matrices."""
+    from oracle import fit as of
+    from oracle import quantize as oq
+
+    rng = np.random.default_rng(seed)
+    threads = os.cpu_count() or 1
+    matrices = 0
+    started = time.perf_counter()
+    generation = 0.0
+    while True:
+        began = time.perf_counter()
+        x = of.to_bfloat16_values(of.decaying_spectrum(rng, TOKENS, CHANNELS))
+        generation += time.perf_counter() - began
+        gram = x.T @ x  # FP32 product (BLAS threads)
+        values, vectors = np.linalg.eigh(gram)
+        values, rows = values[::-1], vectors[:, ::-1].T
+        total = float(np.square(x.astype(np.float64)).sum())
+        rank = of.bucket(of.crossing(values.astype(np.float64), total, 0.98 if matrices % 2 == 0 else 0.95), 32,
+                         CHANNELS)
+        stored = of.stored_basis(rows[:rank])
+        oq.quantize(of.project(x, stored), "per_channel")
+        matrices += 1
+        elapsed = time.perf_counter() - started - generation
+        if elapsed >= seconds_budget or matrices >= 8:
+            break
+    per_matrix = elapsed / matrices
+    return {"value": round(1.0 / (per_matrix * 2 * LAYERS), 4), "unit": "chunks/s", "cores": threads, "kind": "port",
+            "sample": f"{matrices} CausVid-shape matrices [4680, 1536] through oracle.fit (numpy FP32 Gram, LAPACK "
+                      f"eigh, crossing, FP64 projection, quantizer) on {threads} host threads; "
+                      f"{per_matrix * 1e3:.0f} ms/matrix, 60 matrices per chunk"}
+
+
+def fit_leg(device, steps, warmup, cpu_seconds):
+    from reelcache_amd import fit_kernels as fk
+
+    sources, contexts = fit_workload(device)
+    print(f"fit: {len(sources)} source matrices generated", file=sys.stderr, flush=True)
+    for _ in range(warmup):
+        fit_step(sources, contexts, device)
+        print("fit: warmup chunk done", file=sys.stderr, flush=True)
+    stages = {"gram": 0.0, "eigh": 0.0, "verify": 0.0, "energy": 0.0}
+    torch.cuda.synchronize(device)
+    began = time.perf_counter()
+    plan = None
+    for _ in range(steps):
+        plan, _codes = fit_step(sources, contexts, device)
+        print("fit: timed chunk done", file=sys.stderr, flush=True)
+        for name in stages:
+            stages[name] += plan.stages.get(name, 0.0)
+    seconds = (time.perf_counter() - began) / steps
+    matrices = len(sources)
+    # The Gram kernel alone, timed with events on the launch stream.
+    batch = list(sources.values())
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    fk.gram(batch)
+    start.record()
+    for _ in range(3):
+        fk.gram(batch)
+    stop.record()
+    torch.cuda.synchronize(device)
+    gram_ms = start.elapsed_time(stop) / 3
+    unique = TOKENS * CHANNELS * (CHANNELS + 1)
+    tiles = (CHANNELS // 128) * (CHANNELS // 128 + 1) // 2
+    ranks = sorted({p.rank_view for p in plan.plans.values()})
+    observed = {"K": sorted({p.observed_rank for k, p in plan.plans.items() if k.target == "K"}),
+                "V": sorted({p.observed_rank for k, p in plan.plans.items() if k.target == "V"})}
+    result = {
+        "fit_chunks_per_s": round(1.0 / seconds * (matrices / (2 * LAYERS)), 3),
+        "fit": {"chunk_ms": round(seconds * 1e3 * (2 * LAYERS) / matrices, 1), "matrices_per_chunk": 2 * LAYERS,
+                "stage_ms_per_chunk": {k: round(v / steps * 1e3, 2) for k, v in stages.items()},
+                "eigh_ms_per_matrix": round(stages["eigh"] / steps / matrices * 1e3, 3),
+                "gram_kernel_ms_per_chunk": round(gram_ms, 3),
+                "gram_roofline": {"bound": "mfma", "achieved": round(matrices * unique / (gram_ms / 1e3) / 1e12, 1),
+                                  "peak": 2500.0, "unit": "TFLOP/s",
+                                  "frac": round(matrices * unique / (gram_ms / 1e3) / 1e12 / 2500.0, 4),
+                                  "flops": "N*C*(C+1) unique per matrix (issued: 2*N*128^2 per lower tile, "
+                                           f"{tiles} tiles)"},
+                "ranks": ranks, "observed_ranks": observed,
+                "eigh_solver": plan.eigh_solver,
+                "workload": "BASELINE configs[2]: 60 x [4680, 1536] bf16, sigma_i = i^-1.2 + noise 1e-3, "
+                            "K 98 % / V 95 %, bucket 32, per-channel 8-bit codes"},
+    }
+    if cpu_seconds > 0:
+        result["fit"]["cpu_baseline"] = fit_cpu_baseline(cpu_seconds)
+    return result
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
@@ -173,6 +316,8 @@ def main():
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--cpu-seconds", type=float, default=20.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--fit-steps", type=int, default=2, help="timed fit chunks (0 skips the fit leg)")
+    parser.add_argument("--fit-warmup", type=int, default=1)
     parser.add_argument("--copy-probe", action="store_true",
                         help="after the timed region, run 3 plain device copies of 256 MiB (the calibration "
                              "dispatches for rocprofv3 FETCH_SIZE / WRITE_SIZE passes)")
@@ -242,6 +387,7 @@ def main():
                      "mfma_tflops": round(2 * layer_flops() / (kernel_avg / 1e3) / 1e12, 1)},
         "fit_chunks_per_s": None,
     }
+    print(f"restore: {ms_per_step:.2f} ms/step, kernel {kernel_avg * 1e3:.1f} us/layer", file=sys.stderr, flush=True)
     if args.copy_probe:
         source = torch.empty(COPY_PROBE_BYTES, dtype=torch.uint8, device=device).fill_(7)
         target = torch.empty_like(source)
@@ -249,6 +395,11 @@ def main():
             target.copy_(source)
         torch.cuda.synchronize(device)
         del source, target
+    if args.fit_steps > 0:
+        del layers, handles
+        torch.cuda.empty_cache()
+        result.update(fit_leg(device, args.fit_steps, args.fit_warmup,
+                              0.0 if args.no_cpu_baseline else args.cpu_seconds))
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(result), flush=True)

@@ -210,7 +210,7 @@ typedef struct rch_fit_matrix {
     int64_t extrema_ptr;  /* uint32 [2, rank]: ~key(min) then key(max) of each column of P, or 0 */
     int64_t energy_ptr;   /* float64 [2]: sum (X/s)^2 and sum ((X - P Q)/s)^2, s = max|X| */
     int64_t partial_ptr;  /* float64 [ceil(rows / 64), 2]: per-64-row partial energies */
-    int64_t reserved;
+    int64_t resid_ptr;    /* fp32 [rows, channels] (row stride = channels): X - P Q[:rank], or 0 */
 } rch_fit_matrix;         /* 16 x int64 = 128 bytes */
 
 int rch_fit_matrix_size(void);
@@ -249,7 +249,9 @@ int rch_fit_project(const rch_fit_matrix* mats_dev, int n_mats, int channels, in
  * sum ((X - P Q[:rank]) / s)^2 with s = max|X| read from *absmax_ptr (no scaling when s == 0),
  * the reconstruction accumulated in FP64 on v_mfma_f64_16x16x4f64.  Per-64-row partials go to
  * partial_ptr and are summed in a fixed order into energy_ptr (deterministic).  rank == 0
- * measures the source energy alone.
+ * measures the source energy alone.  With resid_ptr set, also writes the residual matrix
+ * fp32(X - P Q[:rank]) (the residual an inherited basis leaves for augmentation,
+ * reelcache/rank_method.py:1347-1358).
  * Replaces the tiled residual guard of project_onto_basis (reelcache/factorization.py:398-419)
  * and measure_source_energy (reelcache/factorization.py:692-724).
  */

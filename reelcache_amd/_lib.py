@@ -48,7 +48,7 @@ PACK_DTYPE = np.dtype([(name, "<i8") for name in PACK_FIELDS])
 # rch_fit_matrix field order (16 x int64).
 FIT_FIELDS = ("src_ptr", "src_dtype", "rows", "src_stride", "basis_ptr", "basis_stride", "rank", "coef_ptr",
               "coef_stride", "gram_ptr", "gram_stride", "absmax_ptr", "extrema_ptr", "energy_ptr", "partial_ptr",
-              "reserved")
+              "resid_ptr")
 FIT_DTYPE = np.dtype([(name, "<i8") for name in FIT_FIELDS])
 
 _i, _i64, _p = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p

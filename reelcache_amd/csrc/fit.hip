@@ -416,6 +416,8 @@ __global__ void __launch_bounds__(kThreads) residual_kernel(const rch_fit_matrix
     const bool scaled = smax != 0.0f;
     const uint32_t x_row = static_cast<uint32_t>(i16 * M->src_stride * E);
     const uint32_t p_row = static_cast<uint32_t>(i16 * M->coef_stride * 4);
+    const bool t_ok = wt + i16 < rows;
+    RCH_GLOBAL float* resid = M->resid_ptr ? gout<float>(M->resid_ptr) + (wt + i16) * channels : nullptr;
 
     double src = 0.0, err = 0.0;
     for (int cb = 0; cb < channels; cb += 16) {
@@ -448,6 +450,7 @@ __global__ void __launch_bounds__(kThreads) residual_kernel(const rch_fit_matrix
             else
                 a = static_cast<double>(half_bits<DT>(__builtin_amdgcn_raw_buffer_load_b16(xs, offset, 0, 0)));
             double e = a - acc[v];
+            if (resid && c < channels && t_ok) resid[c] = static_cast<float>(e);
             if (scaled) {
                 a = a / s;
                 e = e / s;

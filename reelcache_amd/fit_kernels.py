@@ -180,9 +180,11 @@ def split_keys(keys_row, rank: int) -> tuple[np.ndarray, np.ndarray]:
     return decode_min_keys(row[:rank]), decode_max_keys(row[rank:2 * rank])
 
 
-def energies(sources, absmax_keys: torch.Tensor, *, bases=None, ranks=None, coefficients=None) -> torch.Tensor:
+def energies(sources, absmax_keys: torch.Tensor, *, bases=None, ranks=None, coefficients=None,
+             residuals: bool = False):
     """float64 [n, 2]: sum (X/s)^2 and sum ((X - P Q)/s)^2 per source, s = max|X| from ``absmax_keys``
-    (FP64, fixed-order sums); without bases only the source energy (second column = first)."""
+    (FP64, fixed-order sums); without bases only the source energy (second column = first).
+    With ``residuals`` returns ``(totals, [fp32 X - P Q per source])``."""
     device = _device(sources)
     aligned, _, c8 = _check_sources(sources)
     n = len(aligned)
@@ -199,7 +201,12 @@ def energies(sources, absmax_keys: torch.Tensor, *, bases=None, ranks=None, coef
     table["absmax_ptr"] = absmax_keys.data_ptr() + 4 * np.arange(n)
     table["energy_ptr"] = totals.data_ptr() + 16 * np.arange(n)
     table["partial_ptr"] = partials.data_ptr() + 16 * np.concatenate(([0], np.cumsum(tiles)[:-1]))
-    keep = []
+    keep, outputs = [], []
+    if residuals:
+        for index, x in enumerate(aligned):
+            r = torch.empty((x.shape[0], c8), dtype=torch.float32, device=device)
+            table[index]["resid_ptr"] = r.data_ptr()
+            outputs.append(r[:, :sources[index].shape[1]])
     if with_basis:
         for index, (x, basis, rank, p) in enumerate(zip(aligned, bases, ranks, coefficients)):
             rank = int(rank)
@@ -219,7 +226,7 @@ def energies(sources, absmax_keys: torch.Tensor, *, bases=None, ranks=None, coef
     _lib.call("rch_fit_residual", descriptors.data_ptr(), n, c8, max(int(x.shape[0]) for x in aligned),
               _DTYPE_CODES[aligned[0].dtype], _stream(device))
     del keep
-    return totals
+    return (totals, outputs) if residuals else totals
 
 
 def column_extrema(values: torch.Tensor) -> torch.Tensor:

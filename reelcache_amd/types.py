@@ -9,6 +9,8 @@ are interchangeable: the fit code reads only their public attributes (``shape``,
 
 from __future__ import annotations
 
+import hashlib
+import json
 import math
 from dataclasses import dataclass
 from types import MappingProxyType
@@ -36,6 +38,18 @@ def canonical_dtype(value: Any) -> str:
         return _DTYPE_NAMES[name]
     except KeyError:
         raise ConfigurationError(f"unsupported KV dtype: {value!r}") from None
+
+
+def canonical_digest(value: Any) -> str:
+    """SHA-256 hex digest of the canonical JSON of ``value`` (sorted keys, no whitespace, no NaN)."""
+    def plain(item):
+        if isinstance(item, Mapping):
+            return {str(key): plain(child) for key, child in item.items()}
+        if isinstance(item, (list, tuple)):
+            return [plain(child) for child in item]
+        return item
+    text = json.dumps(plain(value), sort_keys=True, separators=(",", ":"), allow_nan=False)
+    return hashlib.sha256(text.encode("utf-8")).hexdigest()
 
 
 def _count(value: Any, name: str, *, zero: bool = False) -> None:
@@ -220,6 +234,14 @@ class CodecSpec:
                 raise ConfigurationError("inter prediction applies only to svd_hevc coefficient streams")
             object.__setattr__(self, "inter_prediction", False)
 
+    def to_dict(self) -> dict[str, Any]:
+        result = {"kind": self.kind, "rank": self.rank, "normalization": self.normalization,
+                  "protected_fraction": self.protected_fraction, "pix_fmt": self.pix_fmt, "qp": self.qp,
+                  "preset": self.preset, "ffmpeg_path": self.ffmpeg_path}
+        if self.kind == "svd_hevc" and self.inter_prediction is not None:
+            result["inter_prediction"] = self.inter_prediction
+        return result
+
 
 @dataclass(frozen=True)
 class EnergyTargets:
@@ -271,4 +293,4 @@ def energy_targets(profile: str) -> EnergyTargets:
 
 
 __all__ = ["CodecSpec", "ENERGY_TARGET_PROFILES", "EnergyTargets", "MatrixKey", "ModelIdentity", "RANK_BUCKET",
-           "TensorContext", "canonical_dtype", "energy_targets"]
+           "TensorContext", "canonical_digest", "canonical_dtype", "energy_targets"]

@@ -1,0 +1,164 @@
+"""GPU tests of the energy-target planner (``reelcache_amd.rank_method.GramPlanner``).
+
+Decisions are checked against the FP64 oracle on inputs built so that each branch is taken with
+a wide margin (``decision_band`` 1e-6 against energy gaps >= 1e-3): fresh fits land on the
+bucket grid with the oracle's crossing as observed rank; an inherited basis that still holds
+the energy is shared (shortest verified prefix); a chunk with new directions is augmented with
+rows orthogonal to the inherited span, or refitted when the augmented bytes exceed a fresh fit's;
+zero matrices and full-width diagnostics take their own branches.  Stored energies agree with
+the oracle's measurement of the returned FP16 rows to 1e-9.  Mirrors the reference's
+SketchTests / FreshFitTests / ReuseTests (tests/test_step4_rank_method.py:80-318).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fit as of
+from oracle import quantize as oq
+from reelcache_amd import fit_kernels as fk
+from reelcache_amd import node_packets as npk
+from reelcache_amd import rank_method as rm
+from reelcache_amd.types import CodecSpec, EnergyTargets, MatrixKey, ModelIdentity, TensorContext, energy_targets
+
+pytestmark = pytest.mark.gpu
+
+PARENT = "manifest:" + "a" * 64
+GROUP = "b" * 64
+
+
+def _model(channels, layers=4):
+    return ModelIdentity("synthetic", "f" * 64, layers, channels, "THD", "bfloat16")
+
+
+def _context(model, key, frames, height, width):
+    return TensorContext(model, key, 0, frames, height, width, "pre_rope" if key.target == "K" else "none")
+
+
+def _stored_energy(host, rows16):
+    scale, source, error = of.energies(host, rows16, of.project(host, rows16))
+    return 1.0 if scale == 0 else 1.0 - error / source
+
+
+def _spectrum(rng, rows, channels, sigma, v=None, noise=1e-3):
+    u, _ = np.linalg.qr(rng.standard_normal((rows, channels)))
+    if v is None:
+        v, _ = np.linalg.qr(rng.standard_normal((channels, channels)))
+    x = (u * sigma) @ v.T + rng.standard_normal((rows, channels)) * (noise * sigma[0] / np.sqrt(rows))
+    tensor = torch.from_numpy(x.astype(np.float32)).to(torch.bfloat16)
+    return tensor, tensor.float().numpy(), v
+
+
+def _plan(config, device, sources, contexts, parents=None, bindings=None):
+    keys = list(sources)
+    parents = parents or {key: None for key in keys}
+    bindings = bindings or {key: rm.ActiveBasisBinding() for key in keys}
+    planner = rm.GramPlanner(config, device=device)
+    return planner.plan({k: sources[k].to(device) for k in keys}, contexts, bindings, parents, chunk_id="c1",
+                        source_ids={k: f"s{k.layer}{k.target}" for k in keys})
+
+
+def _config(targets=None, **kwargs):
+    return rm.RankMethodConfig(targets or energy_targets("causvid"), CodecSpec("svd_hevc", 1), **kwargs)
+
+
+def test_fresh_chunk_at_causvid_shape(device):
+    rng = np.random.default_rng(50)
+    model = _model(1536)
+    sigma = np.arange(1, 1537, dtype=np.float64) ** -1.2
+    sources, hosts, contexts = {}, {}, {}
+    for layer, target in ((0, "K"), (0, "V"), (1, "K"), (1, "V")):
+        key = MatrixKey(layer, target)
+        sources[key], hosts[key], _ = _spectrum(rng, 4680, 1536, sigma)
+        contexts[key] = _context(model, key, 3, 30, 52)
+    plan = _plan(_config(), device, sources, contexts)
+    assert plan.counters["decision_fresh"] == 4 and plan.eigh_solver
+    for key, matrix_plan in plan.plans.items():
+        host = hosts[key]
+        target = 0.98 if key.target == "K" else 0.95
+        values, _ = of.gram_bases(host, 1)
+        assert matrix_plan.observed_rank == of.crossing(values, float(np.square(host.astype(np.float64)).sum()), target)
+        assert matrix_plan.rank_view == matrix_plan.bucket_rank == 32
+        rows = matrix_plan.new_rows.numpy()
+        assert rows.dtype == np.float16 and rows.shape == (32, 1536)
+        np.testing.assert_array_equal(of.canonical_signs(rows), rows)
+        assert matrix_plan.decision_energy == pytest.approx(_stored_energy(host, rows), abs=1e-9)
+        assert matrix_plan.decision_energy >= target + 1e-6
+    # The chunk's codes: projection onto the planned rows, then the device quantizer == oracle.
+    key = MatrixKey(0, "K")
+    rows = plan.plans[key].new_rows.to(device)
+    (p,), keys = fk.project([sources[key].to(device)], [rows], [32], extrema=True)
+    codes, affine, _ = npk.quantize_with_extrema(p, keys[0].cpu().numpy(), CodecSpec("svd_hevc", 32))
+    o_codes, o_affine, _ = oq.quantize(of.project(hosts[key], rows.cpu().numpy()), "per_channel")
+    np.testing.assert_array_equal(affine, o_affine)
+    np.testing.assert_array_equal(codes.cpu().numpy(), o_codes)
+
+
+def _parent_rows(host, count):
+    _, rows = of.gram_bases(host, count)
+    return torch.from_numpy(of.stored_basis(rows))
+
+
+def test_share_shortest_verified_prefix(device):
+    rng = np.random.default_rng(51)
+    model = _model(256)
+    sigma = np.arange(1, 257, dtype=np.float64) ** -1.2
+    key = MatrixKey(0, "K")
+    first, first_host, v = _spectrum(rng, 1000, 256, sigma)
+    second, second_host, _ = _spectrum(rng, 1000, 256, sigma, v=v)
+    parent = _parent_rows(first_host, 64)
+    binding = rm.ActiveBasisBinding(PARENT, 64, GROUP, 64, "c0")
+    plan = _plan(_config(), device, {key: second}, {key: _context(model, key, 1, 1000, 1)}, {key: parent},
+                 {key: binding}).plans[key]
+    assert plan.decision == "share" and plan.new_rows is None and plan.parent_version_ref == PARENT
+    assert plan.rank_view == 32
+    assert plan.decision_energy == pytest.approx(_stored_energy(second_host, parent[:32].numpy()), abs=1e-9)
+    assert plan.decision_energy >= 0.98 + 1e-6
+
+
+def _boosted(rng, v, sigma):
+    boosted = sigma.copy()
+    boosted[40:48] = 0.3  # eight directions outside the inherited top-32 span carry new energy
+    return _spectrum(rng, 1000, 256, boosted, v=v)
+
+
+@pytest.mark.parametrize("fresh_rank,decision", [(None, "augment"), (32, "refit")])
+def test_augment_or_refit(device, fresh_rank, decision):
+    rng = np.random.default_rng(52)
+    model = _model(256)
+    sigma = np.arange(1, 257, dtype=np.float64) ** -1.2
+    key = MatrixKey(1, "V")
+    _, first_host, v = _spectrum(rng, 1000, 256, sigma)
+    second, second_host, _ = _boosted(rng, v, sigma)
+    parent = _parent_rows(first_host, 32)
+    assert _stored_energy(second_host, parent.numpy()) < 0.9  # certification fails by a wide margin
+    binding = rm.ActiveBasisBinding(PARENT, 32, GROUP, fresh_rank, None if fresh_rank is None else "c0")
+    config = _config(EnergyTargets("t", 0.98, 0.98, False))
+    plan = _plan(config, device, {key: second}, {key: _context(model, key, 1, 1000, 1)}, {key: parent},
+                 {key: binding}).plans[key]
+    assert plan.decision == decision
+    rows = plan.new_rows.numpy()
+    if decision == "augment":
+        assert plan.reason == "residual_fit_appended" and plan.estimate["reason"] == "no_fresh_rank_estimate"
+        assert plan.rank_view == 32 + rows.shape[0] and rows.shape[0] % 32 == 0
+        overlap = np.abs(parent.numpy().astype(np.float64) @ rows.astype(np.float64).T).max()
+        assert overlap < 5e-3  # orthogonal to the inherited span up to FP16 rounding
+        stored = np.concatenate((parent.numpy(), rows))
+    else:
+        assert plan.reason == "augmented_bytes_exceed_fresh" and plan.parent_version_ref is None
+        stored = rows
+    assert plan.decision_energy == pytest.approx(_stored_energy(second_host, stored), abs=1e-9)
+    assert plan.decision_energy >= 0.98 + 1e-6
+
+
+def test_zero_and_diagnostic_branches(device):
+    model = _model(64)
+    zero_key, diag_key = MatrixKey(0, "K"), MatrixKey(0, "V")
+    rng = np.random.default_rng(53)
+    sources = {zero_key: torch.zeros((96, 64), dtype=torch.bfloat16),
+               diag_key: _spectrum(rng, 96, 64, np.arange(1, 65, dtype=np.float64) ** -1.0)[0]}
+    contexts = {key: _context(model, key, 1, 96, 1) for key in sources}
+    plan = _plan(_config(EnergyTargets("d", 0.98, 1.0, False)), device, sources, contexts).plans
+    assert plan[zero_key].decision == "zero_input" and plan[zero_key].zero_input
+    assert plan[zero_key].new_rows.tolist()[0][:2] == [1.0, 0.0]
+    assert plan[diag_key].decision == "diagnostic_full_width" and plan[diag_key].rank_view == 64
