@@ -1086,6 +1086,13 @@ def _coefficient_bound(scale, offset):
     return float(max(np.abs(offset).max(), np.abs(np.float32(255) * scale + offset).max())) * 1.0001
 
 
+def _coefficient_bounds(scales, offsets, starts):
+    """:func:`_coefficient_bound` of consecutive segments ``[starts[i], starts[i + 1])`` of
+    concatenated fp32 affine vectors, in one vectorized pass (same fp32 arithmetic)."""
+    magnitude = np.maximum(np.abs(offsets), np.abs(np.float32(255) * scales + offsets))
+    return np.maximum.reduceat(magnitude, starts).astype(np.float64) * 1.0001
+
+
 class _Arena:
     """Host tables packed into one pinned buffer and uploaded with one copy."""
 
@@ -1114,27 +1121,32 @@ class _Arena:
     def size(self):
         return max(16, (self._size + 15) // 16 * 16)
 
-    def upload(self, target, stream):
-        """Fill a pinned host buffer and copy it into ``target`` (uint8 device tensor) on ``stream``."""
+    def upload(self, target):
+        """Fill a pinned host buffer and copy it into ``target`` (uint8 device tensor) on the
+        current stream (the caller's launch stream)."""
         host = torch.empty(self.size, dtype=torch.uint8, pin_memory=True)
         buffer = host.numpy()
         for offset, array in self._parts:
             buffer[offset:offset + array.nbytes] = array.reshape(-1).view(np.uint8)
-        with torch.cuda.stream(stream):
-            target[:self.size].copy_(host, non_blocking=True)
+        target[:self.size].copy_(host, non_blocking=True)
         return host
 
 
 def _balanced_bounds(tile_costs, blocks_per_tile, grid):
     """int32 ``[grid + 1]`` boundaries splitting the (tile, 32-channel block) units into
-    ``grid`` contiguous ranges of near-equal cost."""
-    units = len(tile_costs) * blocks_per_tile
+    ``grid`` contiguous ranges of near-equal cost.  A tile's units share its cost, so the
+    cumulative unit cost is piecewise linear over tiles: each boundary is found at tile
+    granularity and placed inside its tile by linear interpolation."""
+    costs = np.maximum(np.asarray(tile_costs, dtype=np.float64), 1e-9)
+    tiles = len(costs)
+    units = tiles * blocks_per_tile
     if units > 2 ** 31 - 1:
         raise UnsupportedError("restore launch group exceeds 2**31 work units; split the call")
-    cumulative = np.concatenate(([0.0], np.cumsum(np.repeat(np.asarray(tile_costs, dtype=np.float64),
-                                                            blocks_per_tile))))
-    targets = cumulative[-1] * np.arange(grid + 1) / grid
-    bounds = np.rint(np.interp(targets, cumulative, np.arange(units + 1))).astype(np.int64)
+    before = np.concatenate(([0.0], np.cumsum(costs * blocks_per_tile)))  # cost ahead of each tile
+    targets = before[-1] * np.arange(grid + 1) / grid
+    tile = np.clip(np.searchsorted(before, targets, side="right") - 1, 0, tiles - 1)
+    inside = np.minimum((targets - before[tile]) / costs[tile], blocks_per_tile)
+    bounds = np.rint(tile * blocks_per_tile + inside).astype(np.int64)
     bounds[0], bounds[-1] = 0, units
     return np.maximum.accumulate(bounds).astype(np.int32)
 
@@ -1155,6 +1167,13 @@ def _tiles(job_indices, jobs):
 
 
 _JOB_INDEX = {name: index for index, name in enumerate(_lib.JOB_FIELDS)}
+_N_FIELDS = len(_lib.JOB_FIELDS)
+(_C_TOKENS, _C_RANK, _C_FRAMES, _C_GRID_H, _C_GRID_W, _C_SRC_DTYPE, _C_SRC_PTR, _C_SRC_ROW, _C_SRC_COL, _C_SCALE,
+ _C_OFFSET, _C_COEF_EXP, _C_BOUND_INDEX, _C_PACK_PTR, _C_PACK_NBLOCKS, _C_EXP_INDEX, _C_DST_PTR, _C_DST_TOKEN,
+ _C_DST_HEAD, _C_DST_DIM, _C_ROPE, _C_COS, _C_SIN, _C_ROPE_STRIDE, _C_ROW_T, _C_ROW_H, _C_ROW_W, _C_SEC_T, _C_SEC_H,
+ _C_PIC_SLOTS, _C_PIC_PLANES, _C_PIC_COLS, _C_PIC_PLANE_STRIDE, _C_PIC_ROW_STRIDE, _C_PIC_TABLE, _C_FLAGS, _C_PAIRS,
+ _C_PAIRS_BYTES, _C_DST_BYTES, _C_RESERVED) = range(40)
+assert _N_FIELDS == 40 and _JOB_INDEX["pairs_ptr"] == _C_PAIRS and _JOB_INDEX["pic_table_ptr"] == _C_PIC_TABLE
 _OCCUPANCY: dict = {}
 
 
@@ -1173,16 +1192,18 @@ def _fast_flags(row, job, precision):
     """``RCH_GF_*`` of one job: whether it qualifies for the straight-line restore kernel
     (csrc/restore_fast.h), and whether it rotates."""
     kind, _ = _source_kind(job)
-    flags = row["flags"]
-    if precision == "fp32" or job.destination.head_dim % 32 or row.get("bound_index", -1) >= 0:
+    if isinstance(row, dict):  # a partial row by field name
+        row = [row.get(name, -1 if name == "bound_index" else 0) for name in _lib.JOB_FIELDS]
+    flags = row[_C_FLAGS]
+    if precision == "fp32" or job.destination.head_dim % 32 or row[_C_BOUND_INDEX] >= 0:
         return 0
     if not (kind == _lib.SRC_PICTURE or (kind == _lib.SRC_U8 and flags & _lib.JF_SRC_VEC)):
         return 0
-    if not flags & _lib.JF_DST_VEC or row["dst_bytes"] >= _FAST_LIMIT:
+    if not flags & _lib.JF_DST_VEC or row[_C_DST_BYTES] >= _FAST_LIMIT:
         return 0
     if job.rope is None:
         return _lib.GF_FAST
-    if not row.get("pairs_ptr") or row["pairs_bytes"] >= _FAST_LIMIT:
+    if not row[_C_PAIRS] or row[_C_PAIRS_BYTES] >= _FAST_LIMIT:
         return 0
     return _lib.GF_FAST | _lib.GF_ROPE
 
@@ -1208,151 +1229,161 @@ class _CallPlan:
         self.variants = []  # per restore launch: "fast" (straight-line kernel) or "general"
 
     # -- per-job descriptor fields ------------------------------------------------------------
+    # Rows are plain lists indexed by the rch_job field columns (``_JOB_INDEX``); one int64
+    # table is built from them at the end of the call.
     @staticmethod
     def _destination(row, job):
         view = job.destination
         address = _destination_address(view)
         strides = view.strides()
-        row["dst_ptr"] = address
-        row["dst_token_stride"], row["dst_head_stride"], row["dst_dim_stride"] = strides
+        row[_C_DST_PTR] = address
+        row[_C_DST_TOKEN], row[_C_DST_HEAD], row[_C_DST_DIM] = strides
         size = view.tensor.element_size()
-        row["dst_bytes"] = ((job.tokens - 1) * strides[0] + (view.heads - 1) * strides[1]
-                            + (view.head_dim - 1) * strides[2] + 1) * size
+        row[_C_DST_BYTES] = ((job.tokens - 1) * strides[0] + (view.heads - 1) * strides[1]
+                             + (view.head_dim - 1) * strides[2] + 1) * size
         per16 = 16 // size
         if (address % 16 == 0 and strides[2] == 1 and strides[0] % per16 == 0 and strides[1] % per16 == 0
                 and view.head_dim % 16 == 0):
-            row["flags"] |= _lib.JF_DST_VEC
+            row[_C_FLAGS] |= _lib.JF_DST_VEC
 
     def _rope(self, row, job, tables):
         if job.rope is None:
             return
         table = job.rope.table
-        cos, sin = tables.get(id(table), (None, None))
-        if cos is None:
+        entry = tables.get(id(table))
+        if entry is None:
             cos, sin = table.kernel_tables(self.device, self.stream)
-            tables[id(table)] = (cos, sin)
-            self.keepalive.extend((cos, sin))
-        row["cos_ptr"], row["sin_ptr"], row["rope_row_stride"] = cos.data_ptr(), sin.data_ptr(), cos.stride(0)
-        if table.sections is None:
-            row["rope"] = _lib.ROPE_DENSE
-            row["row_t"] = job.rope.rows
-        else:
-            row["rope"] = _lib.ROPE_SEPARABLE
-            row["row_t"], row["row_h"], row["row_w"] = job.rope.rows
-            row["sec_t"], row["sec_h"] = table.sections[0], table.sections[1]
-        if (cos.data_ptr() % 16 == 0 and sin.data_ptr() % 16 == 0 and cos.stride(0) % 4 == 0 and cos.stride(1) == 1
-                and sin.stride(0) == cos.stride(0) and job.destination.head_dim % 16 == 0):
-            row["flags"] |= _lib.JF_ROPE_VEC
-        if job.destination.head_dim % 32 == 0 and cos.stride(0) % 2 == 0 and cos.stride(1) == 1:
-            pairs = tables.get(("pairs", id(table)))
-            if pairs is None:
+            pairs = None
+            if cos.stride(0) % 2 == 0 and cos.stride(1) == 1:
                 pairs = table.kernel_pairs(self.device, self.stream)
-                tables[("pairs", id(table))] = pairs
                 self.keepalive.append(pairs)
-            row["pairs_ptr"], row["pairs_bytes"] = pairs.data_ptr(), pairs.numel() * 4
+            vec = (cos.data_ptr() % 16 == 0 and sin.data_ptr() % 16 == 0 and cos.stride(0) % 4 == 0
+                   and cos.stride(1) == 1 and sin.stride(0) == cos.stride(0))
+            entry = (cos, sin, pairs, vec)
+            tables[id(table)] = entry
+            self.keepalive.extend((cos, sin))
+        cos, sin, pairs, vec = entry
+        row[_C_COS], row[_C_SIN], row[_C_ROPE_STRIDE] = cos.data_ptr(), sin.data_ptr(), cos.stride(0)
+        if table.sections is None:
+            row[_C_ROPE] = _lib.ROPE_DENSE
+            row[_C_ROW_T] = job.rope.rows
+        else:
+            row[_C_ROPE] = _lib.ROPE_SEPARABLE
+            row[_C_ROW_T], row[_C_ROW_H], row[_C_ROW_W] = job.rope.rows
+            row[_C_SEC_T], row[_C_SEC_H] = table.sections[0], table.sections[1]
+        head_dim = job.destination.head_dim
+        if vec and head_dim % 16 == 0:
+            row[_C_FLAGS] |= _lib.JF_ROPE_VEC
+        if pairs is not None and head_dim % 32 == 0:
+            row[_C_PAIRS], row[_C_PAIRS_BYTES] = pairs.data_ptr(), pairs.numel() * 4
 
     def run(self, stage_events=None):
         jobs, precision = self.jobs, self.precision
         fragment = 32 if precision == "fp32" else 16
         fp16_mode = precision in ("fp16", "fp16x2")
         arena = _Arena()
-        # Descriptor rows as dicts (cheap to fill), converted to the int64 table once.
-        rows = [{"flags": 0} for _ in jobs]
-        patches = []  # (job index, field, arena offset)
+        rows = [[0] * _N_FIELDS for _ in jobs]
+        arena_refs = []  # (job index, column, arena byte offset): the field becomes buffer base + offset
+        pack_refs = []   # (job index, pack index): pack_ptr
         tables: dict = {}
 
         # Bases: one pack per distinct basis view, covering the largest rank any job uses from it.
         packs: dict = {}
-        for job in jobs:
-            if job.basis is None:
-                continue
+        basis_key = [None] * len(jobs)
+        for index, job in enumerate(jobs):
             basis = job.basis
+            if basis is None:
+                continue
             if basis.dtype not in BASIS_DTYPES or basis.stride(1) != 1:
                 raise ConfigurationError("GPU kernels need a float16 (or bfloat16) basis with unit column stride")
             key = (basis.data_ptr(), basis.stride(0), basis.shape[1], basis.dtype)
-            packs[key] = max(packs.get(key, 0), job.rank)
+            basis_key[index] = key
+            if job.rank > packs.get(key, 0):
+                packs[key] = job.rank
         pack_keys = list(packs)
         n_packs = len(pack_keys)
         pack_index = {key: index for index, key in enumerate(pack_keys)}
         nblocks = [2 * ((key[2] + 63) // 64) for key in pack_keys]
-        pack_bytes = [((packs[key] + 15) // 16) * blocks * 64 * fragment for key, blocks in zip(pack_keys, nblocks)]
-        pack_offsets = np.concatenate(([0], np.cumsum([(size + 255) // 256 * 256 for size in pack_bytes])))
-        # Device workspace: packed fragments; int32 scratch words: per-block basis exponents of every
-        # pack, then zero-filled fp32 device coefficient bounds (one per job).
-        exp_first = np.concatenate(([0], np.cumsum(nblocks))).astype(np.int64)
-        bound_first = int(exp_first[-1])
-        with torch.cuda.stream(self.stream):
-            workspace = torch.empty(int(pack_offsets[-1]) + 256, dtype=torch.uint8, device=self.device)
-            scratch = torch.zeros(bound_first + len(jobs), dtype=torch.int32, device=self.device)
-        self.keepalive.extend((workspace, scratch))
-        pack_base, scratch_base = workspace.data_ptr(), scratch.data_ptr()
-        pack_desc = np.zeros(n_packs, dtype=_lib.PACK_DTYPE)
-        for index, key in enumerate(pack_keys):
-            row = pack_desc[index]
-            row["src_ptr"], row["row_stride"], row["channels"] = key[0], key[1], key[2]
-            row["src_dtype"] = _DTYPE_CODES[key[3]]
-            row["rank"] = packs[key]
-            row["dst_ptr"] = pack_base + int(pack_offsets[index])
-            row["ksteps"] = (packs[key] + 15) // 16
-            row["nblocks"] = nblocks[index]
-            row["exp_ptr"] = scratch_base + 4 * int(exp_first[index])
+        ksteps = [(packs[key] + 15) // 16 for key in pack_keys]
+        pack_offsets, pack_total = [], 0
+        for blocks, steps in zip(nblocks, ksteps):
+            pack_offsets.append(pack_total)
+            pack_total += (steps * blocks * 64 * fragment + 255) // 256 * 256
+        # int32 scratch words: per-block basis exponents of every pack (written by the pack
+        # kernel), then the fp32 device coefficient bounds (one per job, zero-filled when used).
+        exp_first = [0]
+        for blocks in nblocks:
+            exp_first.append(exp_first[-1] + blocks)
+        bound_first = exp_first[-1]
 
+        affine_jobs = []  # (job index, scale, offset) of quantized / picture sources
         bound_jobs = []
         for index, job in enumerate(jobs):
             row = rows[index]
             source = job.source
-            row["tokens"] = job.tokens
-            row["frames"], row["grid_h"], row["grid_w"] = job.grid
-            row["bound_index"] = -1
+            row[_C_TOKENS] = job.tokens
+            row[_C_FRAMES], row[_C_GRID_H], row[_C_GRID_W] = job.grid
+            row[_C_BOUND_INDEX] = -1
             self._destination(row, job)
             self._rope(row, job, tables)
             if isinstance(source, DenseSource):
                 values = source.values
-                row["src_dtype"] = _DTYPE_CODES[values.dtype]
-                row["src_ptr"] = values.data_ptr()
-                row["src_row_stride"], row["src_col_stride"] = values.stride()
+                row[_C_SRC_DTYPE] = _DTYPE_CODES[values.dtype]
+                row[_C_SRC_PTR] = values.data_ptr()
+                row[_C_SRC_ROW], row[_C_SRC_COL] = values.stride()
                 continue
-            row["rank"] = job.rank
-            key = (job.basis.data_ptr(), job.basis.stride(0), job.basis.shape[1], job.basis.dtype)
-            row["pack_ptr"] = int(pack_desc[pack_index[key]]["dst_ptr"])
-            row["pack_nblocks"] = nblocks[pack_index[key]]
-            row["basis_exp_index"] = int(exp_first[pack_index[key]])
+            row[_C_RANK] = job.rank
+            pack = pack_index[basis_key[index]]
+            pack_refs.append((index, pack))
+            row[_C_PACK_NBLOCKS] = nblocks[pack]
+            row[_C_EXP_INDEX] = exp_first[pack]
             if isinstance(source, PictureSource):
                 layout = source.layout
                 pointers = [[picture.data_ptr() for picture in segment] for segment in source.pictures]
                 base = min(min(segment) for segment in pointers)
-                row["src_ptr"] = base
-                row["src_dtype"] = _lib.DT_U8
-                row["pic_slots"] = layout["channels_per_segment"]
-                row["pic_planes"] = layout["planes"]
-                row["pic_grid_cols"] = layout["grid"][0]
-                row["pic_plane_stride"] = source.plane_stride
-                row["pic_row_stride"] = source.row_stride
+                row[_C_SRC_PTR] = base
+                row[_C_SRC_DTYPE] = _lib.DT_U8
+                row[_C_PIC_SLOTS] = layout["channels_per_segment"]
+                row[_C_PIC_PLANES] = layout["planes"]
+                row[_C_PIC_COLS] = layout["grid"][0]
+                row[_C_PIC_PLANE_STRIDE] = source.plane_stride
+                row[_C_PIC_ROW_STRIDE] = source.row_stride
                 offsets = np.array([[pointer - base for pointer in segment] for segment in pointers], dtype=np.int64)
-                patches.append((index, "pic_table_ptr", arena.add(offsets)))
-                scale, offset = source.scale, source.offset
+                arena_refs.append((index, _C_PIC_TABLE, arena.add(offsets)))
+                affine_jobs.append((index, source.scale, source.offset))
             else:
                 values = source.values
-                row["src_ptr"] = values.data_ptr()
-                row["src_dtype"] = _DTYPE_CODES[values.dtype]
-                row["src_row_stride"], row["src_col_stride"] = values.stride()
+                row[_C_SRC_PTR] = values.data_ptr()
+                row[_C_SRC_DTYPE] = _DTYPE_CODES[values.dtype]
+                row[_C_SRC_ROW], row[_C_SRC_COL] = values.stride()
                 if source.quantized:
-                    scale, offset = source.scale, source.offset
+                    affine_jobs.append((index, source.scale, source.offset))
                     if values.data_ptr() % 16 == 0 and values.stride(1) == 1 and values.stride(0) % 16 == 0:
-                        row["flags"] |= _lib.JF_SRC_VEC
-                else:
-                    scale = offset = None
-            if scale is not None:
-                patches.append((index, "scale_ptr", arena.add(scale[:job.rank])))
-                patches.append((index, "offset_ptr", arena.add(offset[:job.rank])))
+                        row[_C_FLAGS] |= _lib.JF_SRC_VEC
+                elif fp16_mode:
+                    if source.bound is not None:
+                        row[_C_COEF_EXP] = _prescale_exponent(source.bound)
+                    else:
+                        row[_C_BOUND_INDEX] = bound_first + index
+                        bound_jobs.append(index)
+        if affine_jobs:
+            # Every job's fp32 (scale | offset) in one host table; the fp16 modes' prescale bound
+            # max(|offset|, |255 * scale + offset|) of every job in one vectorized pass.
+            ranks = [jobs[index].rank for index, _, _ in affine_jobs]
+            scales = np.concatenate([np.asarray(scale[:rank], dtype=np.float32)
+                                     for (_, scale, _), rank in zip(affine_jobs, ranks)])
+            offsets = np.concatenate([np.asarray(offset[:rank], dtype=np.float32)
+                                      for (_, _, offset), rank in zip(affine_jobs, ranks)])
+            starts = np.concatenate(([0], np.cumsum(ranks)[:-1])).astype(np.int64)
+            table_offset = arena.add(np.concatenate((scales, offsets)))
+            total = int(scales.size)
+            bounds = _coefficient_bounds(scales, offsets, starts) if fp16_mode else None
+            for position, (index, _, _) in enumerate(affine_jobs):
+                first = int(starts[position])
+                arena_refs.append((index, _C_SCALE, table_offset + 4 * first))
+                arena_refs.append((index, _C_OFFSET, table_offset + 4 * (total + first)))
                 if fp16_mode:
-                    row["coef_exp"] = _prescale_exponent(_coefficient_bound(scale[:job.rank], offset[:job.rank]))
-            elif fp16_mode:
-                if source.bound is not None:
-                    row["coef_exp"] = _prescale_exponent(source.bound)
-                else:
-                    row["bound_index"] = bound_first + index
-                    bound_jobs.append(index)
+                    rows[index][_C_COEF_EXP] = _prescale_exponent(float(bounds[position]))
 
         # Launch groups and their balanced persistent grids.  Jobs that qualify for the
         # straight-line kernel (RCH_GF_FAST) are grouped apart, split by RoPE presence.
@@ -1376,8 +1407,9 @@ class _CallPlan:
                 launches_planned.append(("dense", tile_offset, len(tiles), channels, head_dim, out_dtype))
                 continue
             blocks_per_tile = (channels + 31) // 32
-            max_ksteps = max((jobs[i].rank + 15) // 16 for i in members)
-            steps = np.array([(jobs[i].rank + 15) // 16 for i in tiles[:, 0]], dtype=np.float64)
+            job_steps = {i: (jobs[i].rank + 15) // 16 for i in members}
+            max_ksteps = max(job_steps.values())
+            steps = np.array([job_steps[i] for i in tiles[:, 0].tolist()], dtype=np.float64)
             per_cu = self.config.get("workgroups_per_cu") or _occupancy(self.code, kind, max_ksteps, head_dim, out_dtype,
                                                                         group_flags)
             grid = int(max(1, min(len(tiles) * blocks_per_tile, compute_units * max(1, per_cu))))
@@ -1388,29 +1420,46 @@ class _CallPlan:
             self.variants.append("fast" if group_flags & _lib.GF_FAST else "general")
         bound_tiles = _tiles(bound_jobs, jobs) if bound_jobs else None
         bound_tile_offset = arena.add(bound_tiles) if bound_jobs else None
-        packs_offset = arena.add(pack_desc) if n_packs else None
-        desc = np.zeros((len(jobs), len(_lib.JOB_FIELDS)), dtype=np.int64)
-        desc_offset = arena.reserve(desc.nbytes)
-        with torch.cuda.stream(self.stream):
-            device_buffer = torch.empty(arena.size, dtype=torch.uint8, device=self.device)
-        base = device_buffer.data_ptr()
-        for index, name, offset in patches:
-            rows[index][name] = base + offset
-        for index, row in enumerate(rows):
-            line = desc[index]
-            for name, value in row.items():
-                line[_JOB_INDEX[name]] = value
-        arena.put(desc_offset, desc)
-        host = arena.upload(device_buffer, self.stream)
-        self.keepalive.extend((host, device_buffer))
+        pack_desc = np.zeros(n_packs, dtype=_lib.PACK_DTYPE)
+        packs_offset = arena.reserve(pack_desc.nbytes) if n_packs else None
+        desc_offset = arena.reserve(len(jobs) * _N_FIELDS * 8)
+
+        # One device buffer per call: [host tables | packed bases | scratch words].
+        arena_bytes = (arena.size + 255) // 256 * 256
+        scratch_words = bound_first + len(jobs)
+        buffer = torch.empty(arena_bytes + pack_total + 4 * scratch_words + 256, dtype=torch.uint8, device=self.device)
+        base = buffer.data_ptr()
+        pack_base = base + arena_bytes
+        scratch_base = pack_base + pack_total
+        if bound_jobs:
+            start = arena_bytes + pack_total + 4 * bound_first
+            buffer[start:start + 4 * len(jobs)].zero_()  # fill kernel, not a memset (graph-capture safe)
+        for index, key in enumerate(pack_keys):
+            entry = pack_desc[index]
+            entry["src_ptr"], entry["row_stride"], entry["channels"] = key[0], key[1], key[2]
+            entry["src_dtype"] = _DTYPE_CODES[key[3]]
+            entry["rank"] = packs[key]
+            entry["dst_ptr"] = pack_base + pack_offsets[index]
+            entry["ksteps"] = ksteps[index]
+            entry["nblocks"] = nblocks[index]
+            entry["exp_ptr"] = scratch_base + 4 * exp_first[index]
+        for index, column, offset in arena_refs:
+            rows[index][column] = base + offset
+        for index, pack in pack_refs:
+            rows[index][_C_PACK_PTR] = pack_base + pack_offsets[pack]
+        if n_packs:
+            arena.put(packs_offset, pack_desc)
+        arena.put(desc_offset, np.array(rows, dtype=np.int64))
+        host = arena.upload(buffer)
+        self.keepalive.extend((host, buffer))
 
         hip_stream = self.stream.cuda_stream
         launches = 0
         if stage_events is not None:
             stage_events.append(("start", _record(self.stream)))
         if n_packs:
-            _lib.call("rch_basis_pack", base + packs_offset, n_packs, int(max(nblocks)),
-                      int(max((packs[key] + 15) // 16 for key in pack_keys)), self.code, hip_stream)
+            _lib.call("rch_basis_pack", base + packs_offset, n_packs, int(max(nblocks)), int(max(ksteps)), self.code,
+                      hip_stream)
             launches += 1
         if stage_events is not None:
             stage_events.append(("pack", _record(self.stream)))

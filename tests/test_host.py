@@ -194,3 +194,15 @@ def test_fast_eligibility_rules():
     assert rk._fast_flags(dict(row, pairs_ptr=256, pairs_bytes=1024), roped, "fp16") == _lib.GF_FAST | _lib.GF_ROPE
     odd = make_case(rng, grid=(1, 4, 8), heads=2, head_dim=48, rank=32, rope="none").job
     assert rk._fast_flags(row, odd, "fp16x2") == 0  # head_dim % 32 != 0
+
+
+def test_vectorized_coefficient_bounds_match_the_per_job_rule():
+    rng = np.random.default_rng(28)
+    ranks = [128, 192, 1, 77, 300]
+    scales = [rng.uniform(0, 3, size=r).astype(np.float32) for r in ranks]
+    offsets = [rng.uniform(-500, 500, size=r).astype(np.float32) for r in ranks]
+    starts = np.concatenate(([0], np.cumsum(ranks)[:-1]))
+    bounds = rk._coefficient_bounds(np.concatenate(scales), np.concatenate(offsets), starts)
+    for bound, scale, offset in zip(bounds, scales, offsets):
+        assert float(bound) == rk._coefficient_bound(scale, offset)
+        assert rk._prescale_exponent(float(bound)) == rk._prescale_exponent(rk._coefficient_bound(scale, offset))
