@@ -210,13 +210,16 @@ def fit_step(sources, contexts, device):
     plan = rm.GramPlanner(config, device=device, eigh=solver, eigh_label=label).plan(
         sources, contexts, {k: rm.ActiveBasisBinding() for k in keys}, {k: None for k in keys},
         chunk_id="bench", source_ids={k: str(k) for k in keys})
+    torch.cuda.synchronize(device)
+    planned = time.perf_counter()
     rows = [plan.plans[k].new_rows.to(device) for k in keys]
     ranks = [int(r.shape[0]) for r in rows]
     coefficients, extrema = fk.project([sources[k] for k in keys], rows, ranks, extrema=True)
     host_keys = extrema.cpu().numpy()
-    codes = [npk.quantize_with_extrema(p, host_keys[i], config.spec_for(ranks[i]))[0]
-             for i, p in enumerate(coefficients)]
+    codes = [pixels for pixels, _, _ in npk.quantize_many(coefficients, host_keys,
+                                                         [config.spec_for(r) for r in ranks])]
     torch.cuda.synchronize(device)
+    plan.stages["finalize"] = time.perf_counter() - planned  # projection onto the planned rows + quantization
     return plan, codes
 
 
@@ -262,7 +265,7 @@ def fit_leg(device, steps, warmup, cpu_seconds):
     for _ in range(warmup):
         fit_step(sources, contexts, device)
         print("fit: warmup chunk done", file=sys.stderr, flush=True)
-    stages = {"gram": 0.0, "eigh": 0.0, "verify": 0.0, "energy": 0.0}
+    stages = {"energy": 0.0, "gram": 0.0, "topk": 0.0, "eigh": 0.0, "verify": 0.0, "finalize": 0.0}
     torch.cuda.synchronize(device)
     began = time.perf_counter()
     plan = None
@@ -293,6 +296,8 @@ def fit_leg(device, steps, warmup, cpu_seconds):
         "fit": {"chunk_ms": round(seconds * 1e3 * (2 * LAYERS) / matrices, 1), "matrices_per_chunk": 2 * LAYERS,
                 "stage_ms_per_chunk": {k: round(v / steps * 1e3, 2) for k, v in stages.items()},
                 "eigh_ms_per_matrix": round(stages["eigh"] / steps / matrices * 1e3, 3),
+                "solver": "topk_rr: k = 96 Ritz directions per matrix (FP32 Gram products, FP64 CholeskyQR2, "
+                          "batched 96 x 96 eigh)",
                 "gram_kernel_ms_per_chunk": round(gram_ms, 3),
                 "gram_roofline": {"bound": "mfma", "achieved": round(matrices * unique / (gram_ms / 1e3) / 1e12, 1),
                                   "peak": 2500.0, "unit": "TFLOP/s",

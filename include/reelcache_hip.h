@@ -275,6 +275,24 @@ int rch_column_extrema(const float* values_dev, int64_t rows, int cols, int64_t 
 int rch_quantize(const float* values_dev, int64_t rows, int cols, int64_t stride, const double* scale_dev,
                  const double* offset_dev, uint8_t* codes_dev, int64_t code_stride, void* stream);
 
+/* One matrix of a batched quantization: fp32 values [rows, cols] -> uint8 codes. */
+typedef struct rch_quantize_job {
+    int64_t values_ptr;   /* fp32 [rows, >= cols], unit column stride */
+    int64_t rows;
+    int64_t cols;
+    int64_t stride;       /* elements between rows of values */
+    int64_t affine_ptr;   /* float64 [2, cols]: scale then offset */
+    int64_t codes_ptr;    /* uint8 [rows, >= cols] */
+    int64_t code_stride;
+    int64_t reserved;
+} rch_quantize_job;       /* 8 x int64 = 64 bytes */
+
+/*
+ * rch_quantize over a batch of matrices in one launch (grid: 64-row tiles x jobs), e.g. the
+ * coefficients of every matrix of a chunk after projection.
+ */
+int rch_quantize_batched(const rch_quantize_job* jobs_dev, int n_jobs, int64_t max_rows, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

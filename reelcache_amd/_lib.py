@@ -50,6 +50,8 @@ FIT_FIELDS = ("src_ptr", "src_dtype", "rows", "src_stride", "basis_ptr", "basis_
               "coef_stride", "gram_ptr", "gram_stride", "absmax_ptr", "extrema_ptr", "energy_ptr", "partial_ptr",
               "resid_ptr")
 FIT_DTYPE = np.dtype([(name, "<i8") for name in FIT_FIELDS])
+QUANTIZE_FIELDS = ("values_ptr", "rows", "cols", "stride", "affine_ptr", "codes_ptr", "code_stride", "reserved")
+QUANTIZE_DTYPE = np.dtype([(name, "<i8") for name in QUANTIZE_FIELDS])
 
 _i, _i64, _p = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
 _SIGNATURES = {
@@ -70,6 +72,7 @@ _SIGNATURES = {
     "rch_fit_residual": ([_p, _i, _i, _i64, _i, _p], _i),
     "rch_column_extrema": ([_p, _i64, _i, _i64, _p, _p], _i),
     "rch_quantize": ([_p, _i64, _i, _i64, _p, _p, _p, _i64, _p], _i),
+    "rch_quantize_batched": ([_p, _i, _i64, _p], _i),
 }
 # Further entry points registered by other modules are bound when present.
 _OPTIONAL_SIGNATURES: dict = {}

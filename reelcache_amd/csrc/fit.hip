@@ -537,6 +537,26 @@ __global__ void __launch_bounds__(kThreads) quantize_kernel(const float* __restr
     }
 }
 
+__global__ void __launch_bounds__(kThreads) quantize_batched_kernel(const rch_quantize_job* __restrict__ jobs) {
+    const rch_quantize_job* J = jobs + blockIdx.y;
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * 64;
+    if (r0 >= J->rows) return;
+    const int64_t r1 = J->rows - r0 < 64 ? J->rows : r0 + 64;
+    const int cols = static_cast<int>(J->cols);
+    const RCH_GLOBAL float* values = gin<float>(J->values_ptr);
+    const RCH_GLOBAL double* affine = gin<double>(J->affine_ptr);
+    RCH_GLOBAL uint8_t* codes = gout<uint8_t>(J->codes_ptr);
+    for (int c = threadIdx.x; c < cols; c += kThreads) {
+        const double sc = affine[c], of = affine[cols + c];
+        for (int64_t r = r0; r < r1; ++r) {
+            double q = 0.0;
+            if (sc > 0.0) q = rint((static_cast<double>(values[r * J->stride + c]) - of) / sc);
+            q = q < 0.0 ? 0.0 : (q > 255.0 ? 255.0 : q);
+            codes[r * J->code_stride + c] = static_cast<uint8_t>(q);
+        }
+    }
+}
+
 int check_matrices(const rch_fit_matrix* mats, int n, int channels, const char* what) {
     if (!mats || n <= 0 || n > 65535) return fail(RCH_E_CONFIG, "%s: 1 <= n_mats <= 65535 required", what);
     if (channels <= 0 || channels % 8 != 0 || channels > (1 << 20))
@@ -624,6 +644,14 @@ int rch_quantize(const float* values_dev, int64_t rows, int cols, int64_t stride
     hipLaunchKernelGGL(quantize_kernel, dim3(static_cast<unsigned>((rows + 63) / 64)), dim3(kThreads), 0,
                        as_stream(stream), values_dev, rows, cols, stride, scale_dev, offset_dev, codes_dev, code_stride);
     return check_launch("rch_quantize");
+}
+
+int rch_quantize_batched(const rch_quantize_job* jobs_dev, int n_jobs, int64_t max_rows, void* stream) {
+    if (!jobs_dev || n_jobs <= 0 || n_jobs > 65535 || max_rows <= 0 || (max_rows + 63) / 64 > 0x7fffffff)
+        return fail(RCH_E_CONFIG, "rch_quantize_batched: invalid arguments");
+    const dim3 grid(static_cast<unsigned>((max_rows + 63) / 64), static_cast<unsigned>(n_jobs));
+    hipLaunchKernelGGL(quantize_batched_kernel, grid, dim3(kThreads), 0, as_stream(stream), jobs_dev);
+    return check_launch("rch_quantize_batched");
 }
 
 }  // extern "C"

@@ -152,13 +152,18 @@ def project(sources, bases, ranks, *, extrema: bool = False):
     keep, outputs = [], []
     max_rank = max(int(r) for r in ranks)
     keys = torch.zeros((len(aligned), 2 * max_rank), dtype=torch.int32, device=device) if extrema else None
+    strides = [-(-int(rank) // 4) * 4 for rank in ranks]
+    sizes = [int(x.shape[0]) * stride for x, stride in zip(aligned, strides)]
+    storage = torch.empty(sum(sizes), dtype=torch.float32, device=device)  # every P of the batch, 16-byte rows
+    first = 0
     for index, (x, basis, rank) in enumerate(zip(aligned, bases, ranks)):
         rank = int(rank)
         if not 1 <= rank <= basis.shape[0] or basis.shape[1] > c8 or basis.device != device:
             raise ConfigurationError("projection basis does not match its source")
         q = _aligned_basis(basis, rank, c8)
-        stride = -(-rank // 4) * 4
-        p = torch.empty((x.shape[0], stride), dtype=torch.float32, device=device)
+        stride = strides[index]
+        p = storage[first:first + sizes[index]].view(int(x.shape[0]), stride)
+        first += sizes[index]
         keep.append(q)
         outputs.append(p[:, :rank])
         row = table[index]
@@ -254,4 +259,35 @@ def quantize(values: torch.Tensor, scale: torch.Tensor, offset: torch.Tensor) ->
     codes = torch.empty(values.shape, dtype=torch.uint8, device=device)
     _lib.call("rch_quantize", values.data_ptr(), values.shape[0], cols, values.stride(0), scale.data_ptr(),
               offset.data_ptr(), codes.data_ptr(), codes.stride(0), _stream(device))
+    return codes
+
+
+def quantize_batched(values, affines) -> list[torch.Tensor]:
+    """:func:`quantize` of many fp32 matrices in one launch: ``affines[i]`` is the float64
+    ``[2, cols_i]`` host (scale; offset) of ``values[i]``; one host-to-device copy for all."""
+    device = _device(values)
+    if len(values) != len(affines) or not values:
+        raise ConfigurationError("batched quantization needs one affine per matrix")
+    parts, codes = [], []
+    table = np.zeros(len(values), dtype=_lib.QUANTIZE_DTYPE)
+    offsets = [0]
+    for v, affine in zip(values, affines):
+        affine = np.ascontiguousarray(affine, dtype=np.float64)
+        if (v.dtype != torch.float32 or v.ndim != 2 or min(v.shape) < 1 or v.stride(1) != 1
+                or affine.shape != (2, v.shape[1])):
+            raise ConfigurationError("batched quantization takes nonempty fp32 matrices and [2, cols] affines")
+        parts.append(affine.reshape(-1))
+        offsets.append(offsets[-1] + affine.size)
+    host = torch.from_numpy(np.concatenate(parts))
+    device_affine = host.to(device)
+    for index, v in enumerate(values):
+        out = torch.empty(v.shape, dtype=torch.uint8, device=device)
+        codes.append(out)
+        row = table[index]
+        row["values_ptr"], row["rows"], row["cols"], row["stride"] = v.data_ptr(), v.shape[0], v.shape[1], v.stride(0)
+        row["affine_ptr"] = device_affine.data_ptr() + 8 * offsets[index]
+        row["codes_ptr"], row["code_stride"] = out.data_ptr(), out.stride(0)
+    descriptors = _upload(table, device)
+    _lib.call("rch_quantize_batched", descriptors.data_ptr(), len(values), max(int(v.shape[0]) for v in values),
+              _stream(device))
     return codes

@@ -19,7 +19,8 @@ from . import fit_kernels
 from .errors import ConfigurationError
 from .quantize import affine_from_extrema, expanded_affine, normalization_layout, video_layout
 
-__all__ = ["affine_from_extrema", "mosaic_device", "quantize_device", "quantize_with_extrema", "video_layout"]
+__all__ = ["affine_from_extrema", "mosaic_device", "quantize_device", "quantize_many", "quantize_with_extrema",
+           "video_layout"]
 
 
 def _check(coefficients) -> None:
@@ -60,6 +61,30 @@ def quantize_with_extrema(coefficients: torch.Tensor, keys_row, spec) -> tuple[t
     _check(coefficients)
     low, high = fit_kernels.split_keys(np.asarray(keys_row), int(coefficients.shape[1]))
     return _codes(coefficients, low, high, spec)
+
+
+@torch.no_grad()
+def quantize_many(coefficients, keys, specs):
+    """:func:`quantize_with_extrema` of many matrices (e.g. a chunk's) with one quantizer launch:
+    ``keys`` are the host extrema rows of ``fit_kernels.project(..., extrema=True)``.
+    Returns ``[(pixels, affine, layout)]``."""
+    affines, layouts, outputs, values = [], [], [], []
+    for p, row, spec in zip(coefficients, keys, specs):
+        _check(p)
+        rank = int(p.shape[1])
+        low, high = fit_kernels.split_keys(np.asarray(row), rank)
+        if not (np.isfinite(low).all() and np.isfinite(high).all()):
+            raise ConfigurationError("coefficients must be finite")
+        layout = normalization_layout(rank, spec.normalization, spec.protected_fraction)
+        affine = affine_from_extrema(low, high, layout)
+        scale, offset = expanded_affine(affine, layout, rank)
+        affines.append(np.stack((np.asarray(scale, np.float64), np.asarray(offset, np.float64))))
+        layouts.append((affine.astype("<f4", copy=False), layout))
+        values.append(p if p.stride(1) == 1 else p.contiguous())
+    codes = fit_kernels.quantize_batched(values, affines)
+    for pixels, (affine, layout) in zip(codes, layouts):
+        outputs.append((pixels, affine, layout))
+    return outputs
 
 
 def _cell_columns(video) -> np.ndarray:

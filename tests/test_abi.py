@@ -29,3 +29,5 @@ def test_abi_version_and_descriptor_layout():
     assert lib.rch_pack_size() == _lib.PACK_DTYPE.itemsize == 12 * 8
     assert lib.rch_fragment_bytes(_lib.PRECISION_CODES["fp16x2"]) == 16
     assert lib.rch_fragment_bytes(_lib.PRECISION_CODES["fp32"]) == 32
+    assert lib.rch_fit_matrix_size() == _lib.FIT_DTYPE.itemsize == 16 * 8
+    assert _lib.QUANTIZE_DTYPE.itemsize == 8 * 8

@@ -160,3 +160,20 @@ def test_quantizer_bit_exact(device, normalization, fraction):
     low2, high2 = fk.split_keys(fk.column_extrema(values).cpu().numpy(), 32)
     np.testing.assert_array_equal(low2, low)
     np.testing.assert_array_equal(high2, high)
+
+
+def test_batched_quantizer_matches_single_launches(device):
+    rng = np.random.default_rng(17)
+    values, affines = [], []
+    for rows, cols in ((4680, 32), (700, 64), (1, 5), (129, 96)):
+        v = torch.from_numpy((rng.standard_normal((rows, cols)) * 3).astype(np.float32)).to(device)
+        lo, hi = v.amin(0).cpu().numpy(), v.amax(0).cpu().numpy()
+        affine = pq.covering_affine(lo, hi).astype(np.float64)
+        affine[0, 1] = 0.0  # a zero scale maps the column to code 0
+        values.append(v)
+        affines.append(affine)
+    batched = fk.quantize_batched(values, affines)
+    for v, affine, codes in zip(values, affines, batched):
+        single = fk.quantize(v, torch.from_numpy(affine[0].copy()).to(device), torch.from_numpy(affine[1].copy()).to(device))
+        np.testing.assert_array_equal(codes.cpu().numpy(), single.cpu().numpy())
+        np.testing.assert_array_equal(codes.cpu().numpy(), oq.quantize_with_affine(v.cpu().numpy(), affine[0], affine[1]))

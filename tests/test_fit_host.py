@@ -220,9 +220,10 @@ def _config(**kwargs):
 
 
 def test_planner_config_and_binding_rules():
-    assert _config().solver_id() == "fp32_gram_eigh.v1"
+    assert _config().solver_id() == "fp32_gram_topk_rr.v1:m64:s3"  # the reference's default solver
+    assert _config(solver="gram_eigh").solver_id() == "fp32_gram_eigh.v1"
     with pytest.raises(UnsupportedError):
-        _config(solver="topk_rr")
+        _config(solver="warm_start")
     with pytest.raises(UnsupportedError):
         _config(refit_rule="cumulative")
     with pytest.raises(ConfigurationError):

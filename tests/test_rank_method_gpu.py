@@ -62,7 +62,8 @@ def _config(targets=None, **kwargs):
     return rm.RankMethodConfig(targets or energy_targets("causvid"), CodecSpec("svd_hevc", 1), **kwargs)
 
 
-def test_fresh_chunk_at_causvid_shape(device):
+@pytest.mark.parametrize("solver", ["topk_rr", "gram_eigh"])
+def test_fresh_chunk_at_causvid_shape(device, solver):
     rng = np.random.default_rng(50)
     model = _model(1536)
     sigma = np.arange(1, 1537, dtype=np.float64) ** -1.2
@@ -71,7 +72,7 @@ def test_fresh_chunk_at_causvid_shape(device):
         key = MatrixKey(layer, target)
         sources[key], hosts[key], _ = _spectrum(rng, 4680, 1536, sigma)
         contexts[key] = _context(model, key, 3, 30, 52)
-    plan = _plan(_config(), device, sources, contexts)
+    plan = _plan(_config(solver=solver), device, sources, contexts)
     assert plan.counters["decision_fresh"] == 4 and plan.eigh_solver
     for key, matrix_plan in plan.plans.items():
         host = hosts[key]
@@ -122,8 +123,9 @@ def _boosted(rng, v, sigma):
     return _spectrum(rng, 1000, 256, boosted, v=v)
 
 
+@pytest.mark.parametrize("solver", ["topk_rr", "gram_eigh"])
 @pytest.mark.parametrize("fresh_rank,decision", [(None, "augment"), (32, "refit")])
-def test_augment_or_refit(device, fresh_rank, decision):
+def test_augment_or_refit(device, fresh_rank, decision, solver):
     rng = np.random.default_rng(52)
     model = _model(256)
     sigma = np.arange(1, 257, dtype=np.float64) ** -1.2
@@ -133,7 +135,7 @@ def test_augment_or_refit(device, fresh_rank, decision):
     parent = _parent_rows(first_host, 32)
     assert _stored_energy(second_host, parent.numpy()) < 0.9  # certification fails by a wide margin
     binding = rm.ActiveBasisBinding(PARENT, 32, GROUP, fresh_rank, None if fresh_rank is None else "c0")
-    config = _config(EnergyTargets("t", 0.98, 0.98, False))
+    config = _config(EnergyTargets("t", 0.98, 0.98, False), solver=solver)
     plan = _plan(config, device, {key: second}, {key: _context(model, key, 1, 1000, 1)}, {key: parent},
                  {key: binding}).plans[key]
     assert plan.decision == decision
@@ -162,3 +164,29 @@ def test_zero_and_diagnostic_branches(device):
     assert plan[zero_key].decision == "zero_input" and plan[zero_key].zero_input
     assert plan[zero_key].new_rows.tolist()[0][:2] == [1.0, 0.0]
     assert plan[diag_key].decision == "diagnostic_full_width" and plan[diag_key].rank_view == 64
+
+
+def test_topk_directions_match_the_full_eigendecomposition(device):
+    """Top-k Rayleigh-Ritz (k = bucket + margin) against the full Gram eigh of the same matrices:
+    the leading Ritz values and subspaces agree, and the extender doubles the set up to the
+    exact full decomposition."""
+    rng = np.random.default_rng(54)
+    sigma = np.arange(1, 513, dtype=np.float64) ** -1.2
+    sources = [_spectrum(rng, 2000, 512, sigma)[0].to(device) for _ in range(3)]
+    totals = [float(x.double().square().sum()) for x in sources]
+    seeds = [11, 12, 13]
+    topk = rm.topk_directions(sources, totals, [32] * 3, [None] * 3, seeds, margin=64, steps=3, align=32)
+    full = rm.gram_directions(sources, totals)
+    for fast, exact in zip(topk, full):
+        assert fast.width == 96 and not fast.complete and exact.complete
+        top = slice(0, 16)
+        np.testing.assert_allclose(fast.energies[top].cpu().numpy(), exact.energies[top].cpu().numpy(), rtol=1e-4)
+        a = fast.rows[:16].double().cpu().numpy()
+        b = exact.rows[:16].double().cpu().numpy()
+        assert np.abs(a.T @ a - b.T @ b).max() < 1e-3
+        assert fast.crossing(0.9) == exact.crossing(0.9)
+    wider = topk[0].extender(topk[0], 32)
+    assert wider.width == 192 and not wider.complete
+    widest = wider.extender(wider, 32)
+    assert widest.width == 384
+    assert widest.extender(widest, 32).complete  # k reaches C: the full eigendecomposition
