@@ -57,6 +57,11 @@ __device__ __forceinline__ int xcd_unit(int b, int grid) {
     return x * q + (x < r ? x : r) + i;
 }
 
+// s_waitcnt vmcnt(0) with expcnt / lgkmcnt unconstrained (gfx9 encoding: vmcnt in bits 3:0 and
+// 15:14, expcnt 6:4, lgkmcnt 11:8).  The compiler's wait insertion accounts for it, so registers
+// loaded before it are known complete afterwards.
+__device__ __forceinline__ void wait_vector_memory() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // Exact 2**e as float for e in [-126, 127].
 __device__ __forceinline__ float pow2f(int e) { return __int_as_float((e + 127) << 23); }
 

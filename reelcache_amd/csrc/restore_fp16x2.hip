@@ -1,5 +1,5 @@
 // fp16x2 variants of the fused restore kernel (one translation unit per precision).
-#include "restore_fast.h"
+#include "restore_slice.h"
 
 namespace rch {
 
@@ -7,6 +7,10 @@ RestoreVariant pick_restore_fp16x2(int source_kind, int ks) { return pick_source
 
 FastFn pick_fast_fp16x2(int ks, bool rope, int out_dtype, int* chosen) {
     return pick_fast<RCH_PREC_FP16X2>(ks, rope, out_dtype, chosen);
+}
+
+SliceFn pick_slice_fp16x2(int ks, bool rope, int out_dtype, int* chosen, int* max_blocks) {
+    return pick_slice<RCH_PREC_FP16X2>(ks, rope, out_dtype, chosen, max_blocks);
 }
 
 }  // namespace rch

@@ -1,9 +1,11 @@
-"""GPU parity of the straight-line restore kernel (csrc/restore_fast.h).
+"""GPU parity of the straight-line and channel-slice restore kernels (csrc/restore_fast.h,
+csrc/restore_slice.h).
 
 Launch groups whose jobs all qualify (uint8 codes in 16-byte aligned rows or pictures,
-head_dim % 32 == 0, unit-stride aligned destinations) run the straight-line kernel; every
-case here runs the same inputs once through it and once through the general kernel
-(``config={"fast_variant": False}``) and requires equal values, then checks both against the
+head_dim % 32 == 0, unit-stride aligned destinations) run the straight-line kernel, or, with
+``config={"slice_variant": True}``, the channel-slice kernel (uint8 rows); every case here runs
+the same inputs through the straight-line, channel-slice and general kernels
+(``config={"fast_variant": False}``) and requires equal values, then checks them against the
 oracle's elementwise error bound (reelcache/restore_kernels.py:1208-1227).
 """
 
@@ -30,10 +32,13 @@ SHAPES = [
 ]
 
 
-def _pair(seed, precision, out_dtype, shape, device):
+VARIANTS = {"sliced": {"slice_variant": True}, "fast": {}, "general": {"fast_variant": False}}
+
+
+def _copies(seed, precision, out_dtype, shape, device, count=len(VARIANTS)):
     layout, heads, head_dim, rank, rope, grid, token_offset, pitch = shape
     cases = []
-    for _ in range(2):
+    for _ in range(count):
         rng = np.random.default_rng(seed)
         cases.append(make_case(rng, grid=grid, heads=heads, head_dim=head_dim, rank=rank, source="uint8",
                                rope=rope, layout=layout, out_dtype=out_dtype, device=device,
@@ -41,8 +46,8 @@ def _pair(seed, precision, out_dtype, shape, device):
     return cases
 
 
-def _run(case, precision, fast):
-    handle = rk.reconstruct([case.job], precision=precision, config={"fast_variant": fast})
+def _run(case, precision, variant):
+    handle = rk.reconstruct([case.job], precision=precision, config=VARIANTS[variant])
     handle.release()
     return handle.stats["variants"]
 
@@ -58,15 +63,16 @@ def _check_bound(case, precision):
 def test_fast_matches_general_and_oracle(device, precision, out_dtype):
     for index, shape in enumerate(SHAPES):
         seed = zlib.crc32(f"{precision}/{out_dtype}/{index}".encode())
-        fast, general = _pair(seed, precision, out_dtype, shape, device)
-        assert _run(fast, precision, True) == ["fast"], shape
-        assert _run(general, precision, False) == ["general"], shape
-        out_fast, out_general = written(fast), written(general)
-        assert np.array_equal(out_fast, out_general), f"{shape}: fast and general kernels differ"
-        _check_bound(fast, precision)
+        cases = dict(zip(VARIANTS, _copies(seed, precision, out_dtype, shape, device)))
+        for variant, case in cases.items():
+            assert _run(case, precision, variant) == [variant], shape
+        out_general = written(cases["general"])
+        for variant in ("sliced", "fast"):
+            assert np.array_equal(written(cases[variant]), out_general), f"{shape}: {variant} and general kernels differ"
+        _check_bound(cases["sliced"], precision)
         # Tokens outside the slot are untouched.
         layout, token_offset = shape[0], shape[6]
-        tensor = fast.job.destination.tensor
+        tensor = cases["sliced"].job.destination.tensor
         canonical = (tensor.transpose(1, 2) if layout == "BHTD" else tensor).reshape(-1, shape[1] * shape[2])
         tokens = int(np.prod(shape[5]))
         assert bool((canonical[:token_offset] == -123.0).all())
@@ -75,7 +81,8 @@ def test_fast_matches_general_and_oracle(device, precision, out_dtype):
 
 def test_fast_pictures_and_mixed_groups(device):
     """Pictures and uint8 sources, K (RoPE) and V (none) jobs in one call: the call splits into
-    one straight-line launch per (source kind, RoPE) group."""
+    one straight-line launch per (source kind, RoPE) group; with the channel-slice variant
+    enabled, the uint8 rows take it and the pictures stay on the straight-line kernel."""
     rng = np.random.default_rng(31)
     table = rk.RopeTable.from_complex(torch.from_numpy(orc.wan_freqs(64, 64)))
     heads, head_dim, grid, tokens = 4, 64, (2, 12, 14), 336
@@ -92,6 +99,11 @@ def test_fast_pictures_and_mixed_groups(device):
     handle = rk.reconstruct([case.job for case in cases])
     handle.release()
     assert sorted(handle.stats["variants"]) == ["fast", "fast"]
+    for case in cases:
+        _check_bound(case, "fp16x2")
+    handle = rk.reconstruct([case.job for case in cases], config={"slice_variant": True})
+    handle.release()
+    assert sorted(handle.stats["variants"]) == ["fast", "sliced"]
     for case in cases:
         _check_bound(case, "fp16x2")
 
