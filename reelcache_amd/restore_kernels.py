@@ -1094,6 +1094,37 @@ def _coefficient_bounds(scales, offsets, starts):
     return np.maximum.reduceat(magnitude, starts).astype(np.float64) * 1.0001
 
 
+_STAGING_LOCK = threading.Lock()
+_STAGING: dict = {}  # "slab": [pinned uint8 tensor, bytes handed out]
+
+
+def reserve_capture_staging(nbytes=1 << 20):
+    """Reserve pinned host memory for :func:`reconstruct` calls captured in a HIP graph.
+
+    A captured call uploads its descriptor tables from this staging instead of a fresh pinned
+    buffer (pinned allocation is not permitted while a stream captures).  Each captured call
+    takes its own region, which stays owned by the capture for the life of the process (its
+    graph reads it on every replay); eager calls do not use it.  Call outside capture with at
+    least the bytes the captured calls need (about 10 KB per call of 14 jobs)."""
+    if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+        raise ConfigurationError("reserve_capture_staging must be called before the capture")
+    with _STAGING_LOCK:
+        slab = _STAGING.get("slab")
+        if slab is None or slab[0].numel() - slab[1] < nbytes:
+            _STAGING["slab"] = [torch.empty(max(int(nbytes), 1 << 20), dtype=torch.uint8, pin_memory=True), 0]
+
+
+def _capture_staging(nbytes):
+    with _STAGING_LOCK:
+        slab = _STAGING.get("slab")
+        start = 0 if slab is None else (slab[1] + 255) // 256 * 256
+        if slab is None or start + nbytes > slab[0].numel():
+            raise ConfigurationError("a reconstruct() captured in a HIP graph needs pinned staging reserved "
+                                     "beforehand: call reserve_capture_staging(nbytes) before the capture")
+        slab[1] = start + nbytes
+        return slab[0][start:start + nbytes]
+
+
 class _Arena:
     """Host tables packed into one pinned buffer and uploaded with one copy."""
 
@@ -1124,8 +1155,13 @@ class _Arena:
 
     def upload(self, target):
         """Fill a pinned host buffer and copy it into ``target`` (uint8 device tensor) on the
-        current stream (the caller's launch stream)."""
-        host = torch.empty(self.size, dtype=torch.uint8, pin_memory=True)
+        current stream (the caller's launch stream).  Under HIP graph capture the buffer comes
+        from the staging reserved by :func:`reserve_capture_staging` (a capture cannot allocate
+        pinned memory; the graph's copy node reads the buffer on every replay)."""
+        if torch.cuda.is_current_stream_capturing():
+            host = _capture_staging(self.size)
+        else:
+            host = torch.empty(self.size, dtype=torch.uint8, pin_memory=True)
         buffer = host.numpy()
         for offset, array in self._parts:
             buffer[offset:offset + array.nbytes] = array.reshape(-1).view(np.uint8)
@@ -2020,7 +2056,8 @@ __all__ = [
     "apply_rope_reference", "dequantize", "device_config", "error_bound", "expand_affine", "fp32_matmul_precision",
     "pending_deferred",
     "reconstruct",
-    "reconstruct_reference", "recommended_precision", "reference_coefficients", "reference_values", "rope_cos_sin",
+    "reconstruct_reference", "recommended_precision", "reference_coefficients", "reference_values",
+    "reserve_capture_staging", "rope_cos_sin",
     "unpack_pictures", "wan_sections",
     "WARMUP_ROPE_MODES", "WARMUP_SOURCES", "WarmupShape", "warmup",
 ]

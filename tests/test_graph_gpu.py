@@ -1,0 +1,67 @@
+"""GPU test of restores captured in a HIP graph.
+
+A call of K (RoPE) and V jobs is captured once per kernel variant (straight-line, channel-slice,
+general); the graph is replayed several times, with eager work and synchronizations between the
+replays and the destinations overwritten before each, and every replay must reproduce the eager
+result bit for bit.  Captured calls take their descriptor staging from memory reserved
+beforehand (``reserve_capture_staging``); the capture itself allocates no pinned memory and
+records no memset.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import restore as orc
+from reelcache_amd import restore_kernels as rk
+
+from restore_cases import destination, make_case
+
+pytestmark = pytest.mark.gpu
+
+
+def _jobs(device):
+    rng = np.random.default_rng(70)
+    table = rk.RopeTable.from_complex(torch.from_numpy(orc.wan_freqs(128, 64)))
+    heads, head_dim, grid, tokens = 4, 128, (2, 9, 13), 234
+    cache_k = destination("BTHD", 2 * tokens, heads, head_dim, "bfloat16", device)
+    cache_v = destination("BTHD", 2 * tokens, heads, head_dim, "bfloat16", device)
+    jobs = []
+    for chunk in range(2):
+        jobs.append(make_case(rng, grid=grid, heads=heads, head_dim=head_dim, rank=96, source="uint8",
+                              view=rk.NativeView(cache_k, token_offset=chunk * tokens), table=table,
+                              rope_rows=(2 * chunk, 0, 0), out_dtype="bfloat16", device=device).job)
+        jobs.append(make_case(rng, grid=grid, heads=heads, head_dim=head_dim, rank=160, source="uint8",
+                              view=rk.NativeView(cache_v, token_offset=chunk * tokens), rope="none",
+                              out_dtype="bfloat16", device=device).job)
+    return jobs, (cache_k, cache_v)
+
+
+@pytest.mark.parametrize("config", [{}, {"slice_variant": True}, {"fast_variant": False}])
+def test_captured_restore_replays_match_eager(device, config):
+    jobs, caches = _jobs(device)
+    for cache in caches:
+        cache.fill_(-3.0)
+    rk.reconstruct(jobs, config=config).release()
+    torch.cuda.synchronize(device)
+    expected = [cache.clone() for cache in caches]
+
+    rk.reserve_capture_staging(1 << 20)
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.graph(graph, stream=stream):
+        handles = [rk.reconstruct(jobs, config=config)]
+    torch.cuda.synchronize(device)
+    assert handles[0].stats["launches"] >= 2
+    for replay in range(4):
+        for cache in caches:
+            cache.fill_(float(-replay - 1))
+        noise = torch.randn(512, 512, device=device) @ torch.randn(512, 512, device=device)  # eager work
+        torch.cuda.synchronize(device)
+        graph.replay()
+        torch.cuda.synchronize(device)
+        for cache, want in zip(caches, expected):
+            assert torch.equal(cache, want), f"replay {replay} differs from the eager restore"
+        del noise
+    del graph, handles

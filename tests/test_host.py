@@ -265,3 +265,17 @@ def test_vectorized_coefficient_bounds_match_the_per_job_rule():
     for bound, scale, offset in zip(bounds, scales, offsets):
         assert float(bound) == rk._coefficient_bound(scale, offset)
         assert rk._prescale_exponent(float(bound)) == rk._prescale_exponent(rk._coefficient_bound(scale, offset))
+
+
+def test_captured_calls_need_reserved_staging(monkeypatch):
+    monkeypatch.setattr(rk, "_STAGING", {})
+    with pytest.raises(ConfigurationError, match="reserve_capture_staging"):
+        rk._capture_staging(4096)
+    slab = torch.zeros(1 << 12, dtype=torch.uint8)
+    monkeypatch.setattr(rk, "_STAGING", {"slab": [slab, 0]})
+    first = rk._capture_staging(1000)
+    second = rk._capture_staging(1000)
+    assert first.numel() == second.numel() == 1000
+    assert second.data_ptr() - slab.data_ptr() == 1024  # regions start 256-byte aligned
+    with pytest.raises(ConfigurationError):
+        rk._capture_staging(3000)  # 2048 + 3000 exceeds the 4096-byte slab
