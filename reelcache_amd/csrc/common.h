@@ -17,6 +17,8 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 typedef double d4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u4 __attribute__((ext_vector_type(4)));  // native vectors: promotable to registers
 typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f2 __attribute__((ext_vector_type(2)));
 
 // Device addresses arrive as int64 descriptor fields; these views make the compiler emit
 // global (not flat) memory instructions.

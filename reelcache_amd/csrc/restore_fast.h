@@ -80,28 +80,31 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
     };
 
     // Basis fragments of a step: thread loads fragments q = tid + i * 256 of the step's block
-    // (zero beyond the job's rank).  The pack of the fetched tile's job is looked up only when
-    // the fetch cursor enters a new tile.
-    int fetch_tile = -1, fetch_ks = 0, fetch_nblocks = 0;
+    // (zero beyond the job's rank).  The pack of the fetched tile's job and this thread's
+    // offsets within a block column are set up only when the fetch cursor enters a new tile;
+    // a step adds the block's offset (out-of-range offsets stay out of range: the block offset
+    // is below 2^31).
+    int fetch_tile = -1;
+    uint32_t fetch_lane[kPer];
     __amdgpu_buffer_rsrc_t pack = make_rsrc(0, 0);
     auto fetch = [&](const Cursor& c, u4 (&into)[kPer]) __attribute__((always_inline)) {
         if (c.tile != fetch_tile) {
             const rch_job* J = jobs + tiles[2 * c.tile];
-            fetch_ks = static_cast<int>((J->rank + 15) >> 4);
-            fetch_nblocks = static_cast<int>(J->pack_nblocks);
-            pack = make_rsrc(J->pack_ptr, int64_t(fetch_ks) * fetch_nblocks * 1024);
+            const int ks = static_cast<int>((J->rank + 15) >> 4);
+            const int nblocks = static_cast<int>(J->pack_nblocks);
+            pack = make_rsrc(J->pack_ptr, int64_t(ks) * nblocks * 1024);
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) {
+                const int q = tid + i * kThreads;
+                const int s = q >> 6, li = q & 63;
+                fetch_lane[i] = s < ks ? static_cast<uint32_t>(s * nblocks) * 1024u + li * 16 : kOutOfRange;
+            }
             fetch_tile = c.tile;
         }
         const uint32_t block_offset = static_cast<uint32_t>((c.head * head_blocks + c.bp) * 1024);
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            const int q = tid + i * kThreads;
-            const int s = q >> 6, li = q & 63;
-            const uint32_t offset = s < fetch_ks
-                                        ? static_cast<uint32_t>(s * fetch_nblocks) * 1024u + block_offset + li * 16
-                                        : kOutOfRange;
-            into[i] = __builtin_amdgcn_raw_buffer_load_b128(pack, offset, 0, 0);
-        }
+        for (int i = 0; i < kPer; ++i)
+            into[i] = __builtin_amdgcn_raw_buffer_load_b128(pack, fetch_lane[i] + block_offset, 0, 0);
     };
     auto commit = [&](int buffer, const u4 (&from)[kPer]) __attribute__((always_inline)) {
 #pragma unroll
@@ -180,7 +183,7 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
         }
         coef_exp = kFp16 ? static_cast<int>(J->coef_exp) : 0;
         head_bytes = static_cast<int>(J->dst_head_stride) * kEsize;
-        const float pre = pow2f(coef_exp);
+        const float pre = pow2f(coef_exp);  // folded into the staged affine
         const int rank = static_cast<int>(J->rank);
         for (int i = tid; i < per_tile; i += kThreads) block_exp[i] = scratch[J->basis_exp_index + i];
         if (J->pic_slots == 0) {  // uint8 rows, 16-byte aligned
@@ -203,14 +206,9 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
                 const int q = tid + i * kThreads;
                 const int token = q / kGroups, g = q - token * kGroups;
                 if (q < kTileTokens * kGroups) {
-                    u4 b = bytes[i];
-                    const int k0 = 16 * g;
-                    // Row padding beyond the rank reads as zero codes.
-#pragma unroll
-                    for (int w = 0; w < 4; ++w) {
-                        const int keep = rank - (k0 + 4 * w);
-                        b[w] = keep >= 4 ? b[w] : (keep <= 0 ? 0u : (b[w] & ((1u << (8 * keep)) - 1u)));
-                    }
+                    // Bytes past the rank (row padding) are staged as they are: their affine
+                    // entries are zero, so they dequantize to 0 * q + 0 = 0.
+                    const u4 b = bytes[i];
                     u2* out = reinterpret_cast<u2*>(codes + token * kPitch + 16 * g);
                     out[0] = u2{b[0], b[1]};
                     out[1] = u2{b[2], b[3]};
@@ -235,8 +233,8 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
             }
         }
         for (int i = tid; i < kRanks; i += kThreads) {
-            affine[i] = i < rank ? gin<float>(J->scale_ptr)[i] : 0.0f;
-            affine[kRanks + i] = i < rank ? gin<float>(J->offset_ptr)[i] : 0.0f;
+            affine[i] = i < rank ? __fmul_rn(gin<float>(J->scale_ptr)[i], pre) : 0.0f;
+            affine[kRanks + i] = i < rank ? __fmul_rn(gin<float>(J->offset_ptr)[i], pre) : 0.0f;
         }
         __syncthreads();
         const uint8_t* mine = codes + (wave * 32 + col) * kPitch;
@@ -248,17 +246,15 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
             const f4 sc1 = *reinterpret_cast<const f4*>(affine + kl + 4);
             const f4 of0 = *reinterpret_cast<const f4*>(affine + kRanks + kl);
             const f4 of1 = *reinterpret_cast<const f4*>(affine + kRanks + kl + 4);
+            // Lanes past the job's tokens convert whatever codes they staged: only their own
+            // (never stored) output columns depend on them.
             float a[8];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 a[j] = dequant((b[0] >> (8 * j)) & 0xffu, sc0[j], of0[j]);
                 a[j + 4] = dequant((b[1] >> (8 * j)) & 0xffu, sc1[j], of1[j]);
             }
-            if (!valid) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) a[j] = 0.0f;
-            }
-            set_frag(cf[s], a, pre);
+            set_frag_scaled(cf[s], a);
         }
     };
 

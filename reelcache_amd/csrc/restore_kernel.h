@@ -82,6 +82,38 @@ __device__ __forceinline__ void set_frag(CoefFrag<RCH_PREC_FP32>& f, const float
     for (int j = 0; j < 8; ++j) f.v[j] = a[j];
 }
 
+// Fragments of 8 values that already carry the power-of-two prescale (quantized sources fold it
+// into the staged affine: fl(fl(q * s * 2^e) + o * 2^e) = 2^e * fl(fl(q * s) + o) exactly while the
+// values stay normal).  Same bits as set_frag(f, a / 2^e, 2^e); conversions run two values at a
+// time (v_cvt_pk_f16_f32 rounds to nearest even like the scalar conversion).
+__device__ __forceinline__ void set_frag_scaled(CoefFrag<RCH_PREC_FP16>& f, const float (&a)[8]) {
+    h8 hi;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const h2 head = __builtin_convertvector((f2{a[2 * p], a[2 * p + 1]}), h2);
+        hi[2 * p] = head[0];
+        hi[2 * p + 1] = head[1];
+    }
+    f.hi = hi;
+}
+__device__ __forceinline__ void set_frag_scaled(CoefFrag<RCH_PREC_FP16X2>& f, const float (&a)[8]) {
+    h8 hi, lo;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const f2 v = {a[2 * p], a[2 * p + 1]};
+        const h2 head = __builtin_convertvector(v, h2);
+        const h2 tail = __builtin_convertvector(v - __builtin_convertvector(head, f2), h2);  // v - hi is exact
+        hi[2 * p] = head[0];
+        hi[2 * p + 1] = head[1];
+        lo[2 * p] = tail[0];
+        lo[2 * p + 1] = tail[1];
+    }
+    f.hi = hi;
+    f.lo = lo;
+}
+__device__ __forceinline__ void set_frag_scaled(CoefFrag<RCH_PREC_BF16>& f, const float (&a)[8]) { set_frag(f, a, 1.0f); }
+__device__ __forceinline__ void set_frag_scaled(CoefFrag<RCH_PREC_FP32>& f, const float (&a)[8]) { set_frag(f, a, 1.0f); }
+
 __device__ __forceinline__ float load_value(int64_t base, int64_t index, int dtype) {
     if (dtype == RCH_DT_F32) return gin<float>(base)[index];
     if (dtype == RCH_DT_F16) return static_cast<float>(gin<_Float16>(base)[index]);
@@ -442,8 +474,8 @@ restore_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict__ til
         }
         for (int i = tid; i < kRanks; i += kThreads) {
             const int k = k_lo + i;
-            affine[i] = k < rank ? gin<float>(J->scale_ptr)[k] : 0.0f;
-            affine[kRanks + i] = k < rank ? gin<float>(J->offset_ptr)[k] : 0.0f;
+            affine[i] = k < rank ? __fmul_rn(gin<float>(J->scale_ptr)[k], pre) : 0.0f;
+            affine[kRanks + i] = k < rank ? __fmul_rn(gin<float>(J->offset_ptr)[k], pre) : 0.0f;
         }
     };
 
@@ -484,7 +516,7 @@ restore_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict__ til
 #pragma unroll
                     for (int j = 0; j < 8; ++j) a[j] = 0.0f;
                 }
-                set_frag(cf[s], a, pre);
+                set_frag_scaled(cf[s], a);  // the prescale is in the staged affine
             }
         } else {  // float coefficients, read per lane and used as is
             const int rank = static_cast<int>(J->rank);

@@ -107,9 +107,11 @@ restore_slice_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict
                     const int rank = static_cast<int>(J->rank);
                     const RCH_GLOBAL float* scale = gin<float>(J->scale_ptr);
                     const RCH_GLOBAL float* offset = gin<float>(J->offset_ptr);
+                    // The power-of-two coefficient prescale (fp16 modes) is folded in here.
+                    const float pre = pow2f(kFp16 ? static_cast<int>(J->coef_exp) : 0);
                     for (int i = tid; i < kRanks; i += kSliceThreads) {
-                        affine[slot][0][i] = i < rank ? scale[i] : 0.0f;
-                        affine[slot][1][i] = i < rank ? offset[i] : 0.0f;
+                        affine[slot][0][i] = i < rank ? __fmul_rn(scale[i], pre) : 0.0f;
+                        affine[slot][1][i] = i < rank ? __fmul_rn(offset[i], pre) : 0.0f;
                     }
                 }
                 ++slot;
@@ -141,8 +143,6 @@ restore_slice_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict
         // fragment lane (token, h) of step s holds ranks 16 s + 8 h .. + 7.
         auto dequant = [&](int t, int slot, const u2 (&codes)[kItems], u4 (&coef)[KS][kParts][64])
                            __attribute__((always_inline)) {
-            const rch_job* J = jobs + tile_job(t);
-            const float pre = pow2f(kFp16 ? static_cast<int>(J->coef_exp) : 0);
 #pragma unroll
             for (int i = 0; i < kItems; ++i) {
                 const int half = dq_half0 + i * (kSliceThreads / 32);
@@ -159,7 +159,7 @@ restore_slice_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict
                     a[j + 4] = rch::dequant((codes[i][1] >> (8 * j)) & 0xffu, s1[j], o1[j]);
                 }
                 CoefFrag<PREC> f;
-                set_frag(f, a, pre);
+                set_frag_scaled(f, a);
                 u4* out = &coef[half >> 1][0][32 * (half & 1) + dq_token];
                 out[0] = __builtin_bit_cast(u4, f.hi);
                 if constexpr (kSplit) out[64] = __builtin_bit_cast(u4, f.lo);
