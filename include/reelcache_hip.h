@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-#define RCH_ABI_VERSION 4
+#define RCH_ABI_VERSION 5
 
 /* Status codes (mapped to reelcache errors by the host). */
 #define RCH_OK 0
@@ -66,6 +66,8 @@ extern "C" {
                               with RoPE, an interleaved pairs table under 2**31 bytes with an even row
                               stride; the group: head_dim % 32 == 0, channels == heads * head_dim */
 #define RCH_GF_ROPE 2      /* with RCH_GF_FAST: every job of the group has RoPE (otherwise none has) */
+#define RCH_GF_HEAD_PAIRS 4 /* with RCH_GF_FAST and an even head count: each work unit covers one
+                               32-channel dim block of two adjacent heads (see rch_restore) */
 
 /*
  * One reconstruction job: one restored [N, C] matrix written into one native
@@ -157,7 +159,9 @@ int rch_coefficient_bound(const rch_job* jobs_dev, int n_jobs, const int32_t* ti
  *   tiles_dev  int32 [n_tiles, 2]: (job, first token) of every 128-token tile.
  *   bounds_dev int32 [grid + 1]: workgroup w processes work units
  *              [bounds[w'], bounds[w' + 1]) (w' = XCD-swizzled index), where unit
- *              u = tile * ceil(channels / 32) + 32-channel block.
+ *              u = tile * ceil(channels / 32) + 32-channel block; with
+ *              RCH_GF_HEAD_PAIRS, u = tile * (channels / 64) + unit of the tile
+ *              (dim block u' / (heads / 2), heads 2 (u' % (heads / 2)) and the next).
  * max_ksteps = max ceil(rank / 16) over the group selects the compiled variant;
  * group_flags (RCH_GF_*) selects the straight-line variant for groups that qualify.
  * scratch_dev holds the basis exponents and device coefficient bounds the

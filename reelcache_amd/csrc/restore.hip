@@ -238,12 +238,13 @@ static int pick_launch(int precision, int source_kind, int max_ksteps, int head_
     if ((group_flags & RCH_GF_FAST) && head_dim % 32 == 0 &&
         (source_kind == RCH_SRC_U8 || source_kind == RCH_SRC_PICTURE)) {
         const bool rope = (group_flags & RCH_GF_ROPE) != 0;
+        const bool pairs = (group_flags & RCH_GF_HEAD_PAIRS) != 0;
         FastFn fn = nullptr;
         int ks = 0;
         switch (precision) {
-            case RCH_PREC_FP16: fn = pick_fast_fp16(max_ksteps, rope, out_dtype, &ks); break;
-            case RCH_PREC_FP16X2: fn = pick_fast_fp16x2(max_ksteps, rope, out_dtype, &ks); break;
-            case RCH_PREC_BF16: fn = pick_fast_bf16(max_ksteps, rope, out_dtype, &ks); break;
+            case RCH_PREC_FP16: fn = pick_fast_fp16(max_ksteps, rope, out_dtype, pairs, &ks); break;
+            case RCH_PREC_FP16X2: fn = pick_fast_fp16x2(max_ksteps, rope, out_dtype, pairs, &ks); break;
+            case RCH_PREC_BF16: fn = pick_fast_bf16(max_ksteps, rope, out_dtype, pairs, &ks); break;
             default: break;
         }
         if (fn) {
@@ -289,6 +290,8 @@ int rch_restore(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev, i
     if (!valid_out(out_dtype)) return fail(RCH_E_CONFIG, "rch_restore: output dtype must be f32, f16 or bf16");
     if ((group_flags & RCH_GF_FAST) && channels % head_dim)
         return fail(RCH_E_CONFIG, "rch_restore: RCH_GF_FAST needs channels == heads * head_dim");
+    if ((group_flags & RCH_GF_HEAD_PAIRS) && (!(group_flags & RCH_GF_FAST) || (channels / head_dim) % 2))
+        return fail(RCH_E_CONFIG, "rch_restore: RCH_GF_HEAD_PAIRS needs RCH_GF_FAST and an even head count");
     Launch launch;
     const int status = pick_launch(precision, source_kind, max_ksteps, head_dim, out_dtype, group_flags, &launch);
     if (status) return status;

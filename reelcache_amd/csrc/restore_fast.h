@@ -33,17 +33,24 @@ constexpr int kFastMaxBlocks = 256;
 
 // Three resident workgroups per CU where the LDS footprint allows it (KS <= 12: at most
 // 51 KB each) and the step fits the 168-VGPR budget that implies without spills (the two
-// RoPE pair sets add 32 VGPRs, so RoPE variants get three only up to KS = 8).
-template <int KS, bool ROPE> constexpr int kFastOccupancy = ((KS <= 12 && !ROPE) || (KS <= 8 && ROPE)) ? 3 : 2;
+// RoPE pair sets add 32 VGPRs, so RoPE variants get three only up to KS = 8).  Head-pair steps
+// (HP = 2) hold two accumulators and twice the staged fragments: two workgroups.
+template <int KS, bool ROPE, int HP>
+constexpr int kFastOccupancy = HP == 2 ? 2 : (((KS <= 12 && !ROPE) || (KS <= 8 && ROPE)) ? 3 : 2);
 
-template <int PREC, int KS, bool ROPE, int OUT>
-__global__ void __launch_bounds__(kThreads, (kFastOccupancy<KS, ROPE>))
+// HP = heads per step: 1, or 2 (RCH_GF_HEAD_PAIRS, an even head count): a step then computes the
+// same 32-channel dim block of two adjacent heads, so the per-step bookkeeping, barrier and
+// waits are shared by twice the matrix work and each RoPE pair set serves both heads.
+template <int PREC, int KS, bool ROPE, int OUT, int HP>
+__global__ void __launch_bounds__(kThreads, (kFastOccupancy<KS, ROPE, HP>))
 restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict__ tiles,
                     const int32_t* __restrict__ bounds, const int32_t* __restrict__ scratch, int heads,
                     int head_dim) {
     static_assert(PREC != RCH_PREC_FP32, "the fp32 mode runs restore_kernel");
+    static_assert(HP == 1 || HP == 2, "one or two heads per step");
     constexpr int kStepFrags = 64;                       // u4 fragments of one 16-rank step of one block
-    constexpr int kBuffer = KS * kStepFrags;
+    constexpr int kHeadFrags = KS * kStepFrags;          // fragments of one block (one head)
+    constexpr int kBuffer = HP * kHeadFrags;
     constexpr int kPer = kBuffer / kThreads;
     static_assert(kBuffer % kThreads == 0, "KS must be a multiple of 4: every thread moves whole fragments");
     constexpr int kRanks = KS * 16;
@@ -60,16 +67,18 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
     const int steps = bounds[range + 1] - first_unit;
     if (steps <= 0) return;
     const int head_blocks = head_dim >> 5;
-    const int per_tile = heads * head_blocks;
+    const int head_steps = heads / HP;  // steps per dim block
+    const int per_tile = head_steps * head_blocks;  // work units per tile (blocks / HP)
     const int last_tile = (first_unit + steps - 1) / per_tile;
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63, h = lane >> 5, col = lane & 31;
 
-    // Unit u of a tile is (dim block u / heads, head u % heads).  Prefetch cursors past the
-    // range end stay on the range's last tile (their fragments are fetched and never used).
+    // Unit u of a tile is (dim block u / head_steps, first head HP * (u % head_steps)).  Prefetch
+    // cursors past the range end stay on the range's last tile (their fragments are fetched and
+    // never used).
     auto advance = [&](Cursor c) __attribute__((always_inline)) {
-        c.head += 1;
+        c.head += HP;
         const bool next_bp = c.head == heads;
         c.head = next_bp ? 0 : c.head;
         c.bp += next_bp ? 1 : 0;
@@ -79,11 +88,11 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
         return c;
     };
 
-    // Basis fragments of a step: thread loads fragments q = tid + i * 256 of the step's block
-    // (zero beyond the job's rank).  The pack of the fetched tile's job and this thread's
-    // offsets within a block column are set up only when the fetch cursor enters a new tile;
-    // a step adds the block's offset (out-of-range offsets stay out of range: the block offset
-    // is below 2^31).
+    // Basis fragments of a step: thread loads fragments q = tid + i * 256 of the step's block(s)
+    // (head j = q / kHeadFrags of the step; zero beyond the job's rank).  The pack of the fetched
+    // tile's job and this thread's offsets within a block column are set up only when the fetch
+    // cursor enters a new tile; a step adds the first block's offset (out-of-range offsets stay
+    // out of range: the block offset is below 2^31).
     int fetch_tile = -1;
     uint32_t fetch_lane[kPer];
     __amdgpu_buffer_rsrc_t pack = make_rsrc(0, 0);
@@ -96,8 +105,9 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
 #pragma unroll
             for (int i = 0; i < kPer; ++i) {
                 const int q = tid + i * kThreads;
-                const int s = q >> 6, li = q & 63;
-                fetch_lane[i] = s < ks ? static_cast<uint32_t>(s * nblocks) * 1024u + li * 16 : kOutOfRange;
+                const int j = q / kHeadFrags, s = (q % kHeadFrags) >> 6, li = q & 63;
+                fetch_lane[i] = s < ks ? static_cast<uint32_t>(s * nblocks + j * head_blocks) * 1024u + li * 16
+                                       : kOutOfRange;
             }
             fetch_tile = c.tile;
         }
@@ -185,7 +195,7 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
         head_bytes = static_cast<int>(J->dst_head_stride) * kEsize;
         const float pre = pow2f(coef_exp);  // folded into the staged affine
         const int rank = static_cast<int>(J->rank);
-        for (int i = tid; i < per_tile; i += kThreads) block_exp[i] = scratch[J->basis_exp_index + i];
+        for (int i = tid; i < heads * head_blocks; i += kThreads) block_exp[i] = scratch[J->basis_exp_index + i];
         if (J->pic_slots == 0) {  // uint8 rows, 16-byte aligned
             const int64_t rs = J->src_row_stride;
             constexpr int kGroups = kRanks / 16;
@@ -260,56 +270,68 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
 
     // One step: product of the staged block, scale, RoPE, cast, store.
     auto finish = [&](const Cursor& c, int buffer, const f4 (&rope)[4]) __attribute__((always_inline)) {
-        // Undo the coefficient prescale and the block's basis exponent (exact powers of two).
-        const int e = coef_exp + block_exp[c.head * head_blocks + c.bp];
         // Basis fragments are read from LDS three steps ahead of their products (a rotating
-        // window of four registers).
+        // window of four registers per head).
         constexpr int kAhead = 3;
         const u4* frags = &lds[buffer][lane];
-        u4 window[kAhead + 1];
+        u4 window[HP][kAhead + 1];
 #pragma unroll
-        for (int j = 0; j < kAhead; ++j) window[j] = frags[j * kStepFrags];
-        f16v acc = {};
+        for (int j = 0; j < kAhead; ++j) {
+#pragma unroll
+            for (int x = 0; x < HP; ++x) window[x][j] = frags[x * kHeadFrags + j * kStepFrags];
+        }
+        f16v acc[HP];
+#pragma unroll
+        for (int x = 0; x < HP; ++x) acc[x] = f16v{};
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
-            if (s + kAhead < KS) window[(s + kAhead) % (kAhead + 1)] = frags[(s + kAhead) * kStepFrags];
-            acc = mfma_frag<PREC>(window[s % (kAhead + 1)], cf[s], acc);
-        }
-        float v[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] = __builtin_amdgcn_ldexpf(acc[i], -e);
-        if constexpr (ROPE) {
-#pragma unroll
-            for (int p = 0; p < 4; ++p) {
-                rotate(v[4 * p], v[4 * p + 1], rope[p][0], rope[p][1]);
-                rotate(v[4 * p + 2], v[4 * p + 3], rope[p][2], rope[p][3]);
+            for (int x = 0; x < HP; ++x) {
+                if (s + kAhead < KS) window[x][(s + kAhead) % (kAhead + 1)] = frags[x * kHeadFrags + (s + kAhead) * kStepFrags];
+                acc[x] = mfma_frag<PREC>(window[x][s % (kAhead + 1)], cf[s], acc[x]);
             }
         }
         const uint32_t offset = dst_lane + static_cast<uint32_t>(c.head * head_bytes + c.bp * 32 * kEsize);
-        if constexpr (OUT == RCH_DT_F32) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const f4 out = {v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, out), dst, offset + 16 * q, 0, 0);
-            }
-        } else if constexpr (OUT == RCH_DT_BF16) {
-            bf8 a, b;
+        for (int x = 0; x < HP; ++x) {
+            // Undo the coefficient prescale and the block's basis exponent (exact powers of two).
+            const int e = coef_exp + block_exp[(c.head + x) * head_blocks + c.bp];
+            float v[16];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                a[i] = static_cast<__bf16>(v[i]);
-                b[i] = static_cast<__bf16>(v[i + 8]);
-            }
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, a), dst, offset, 0, 0);
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, b), dst, offset + 16, 0, 0);
-        } else {
-            h8 a, b;
+            for (int i = 0; i < 16; ++i) v[i] = __builtin_amdgcn_ldexpf(acc[x][i], -e);
+            if constexpr (ROPE) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                a[i] = static_cast<_Float16>(v[i]);
-                b[i] = static_cast<_Float16>(v[i + 8]);
+                for (int p = 0; p < 4; ++p) {
+                    rotate(v[4 * p], v[4 * p + 1], rope[p][0], rope[p][1]);
+                    rotate(v[4 * p + 2], v[4 * p + 3], rope[p][2], rope[p][3]);
+                }
             }
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, a), dst, offset, 0, 0);
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, b), dst, offset + 16, 0, 0);
+            const uint32_t at = offset + static_cast<uint32_t>(x * head_bytes);
+            if constexpr (OUT == RCH_DT_F32) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const f4 out = {v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, out), dst, at + 16 * q, 0, 0);
+                }
+            } else if constexpr (OUT == RCH_DT_BF16) {
+                bf8 a, b;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    a[i] = static_cast<__bf16>(v[i]);
+                    b[i] = static_cast<__bf16>(v[i + 8]);
+                }
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, a), dst, at, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, b), dst, at + 16, 0, 0);
+            } else {
+                h8 a, b;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    a[i] = static_cast<_Float16>(v[i]);
+                    b[i] = static_cast<_Float16>(v[i + 8]);
+                }
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, a), dst, at, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, b), dst, at + 16, 0, 0);
+            }
         }
     };
 
@@ -318,8 +340,8 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
     {
         now.tile = first_unit / per_tile;
         const int local = first_unit - now.tile * per_tile;
-        now.bp = local / heads;
-        now.head = local - now.bp * heads;
+        now.bp = local / head_steps;
+        now.head = (local - now.bp * head_steps) * HP;
     }
     Cursor ahead1 = advance(now), ahead2 = advance(ahead1);
     u4 ring[kPer];
@@ -346,7 +368,7 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
             if constexpr (ROPE) {
                 if (now.bp + 1 < head_blocks) rope_load(now.bp + 1, rope_next);
             }
-            const int run = min(heads - now.head, steps - st);
+            const int run = min((heads - now.head) / HP, steps - st);
             for (int i = 0; i < run; ++i, ++st) {
                 commit((st + 1) & 1, ring);
                 fetch(ahead2, ring);
@@ -368,34 +390,44 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
 
 typedef void (*FastFn)(const rch_job*, const int32_t*, const int32_t*, const int32_t*, int, int);
 
-template <int PREC, bool ROPE, int OUT>
+template <int PREC, bool ROPE, int OUT, int HP>
 FastFn fast_ks(int ks, int* chosen) {
-    if (ks <= 4) { *chosen = 4; return restore_fast_kernel<PREC, 4, ROPE, OUT>; }
-    if (ks <= 8) { *chosen = 8; return restore_fast_kernel<PREC, 8, ROPE, OUT>; }
-    if (ks <= 12) { *chosen = 12; return restore_fast_kernel<PREC, 12, ROPE, OUT>; }
-    if constexpr (PREC != RCH_PREC_FP16X2) {
-        if (ks <= 16) { *chosen = 16; return restore_fast_kernel<PREC, 16, ROPE, OUT>; }
+    if (ks <= 4) { *chosen = 4; return restore_fast_kernel<PREC, 4, ROPE, OUT, HP>; }
+    if (ks <= 8) { *chosen = 8; return restore_fast_kernel<PREC, 8, ROPE, OUT, HP>; }
+    if (ks <= 12) { *chosen = 12; return restore_fast_kernel<PREC, 12, ROPE, OUT, HP>; }
+    if constexpr (PREC != RCH_PREC_FP16X2 && HP == 1) {
+        if (ks <= 16) { *chosen = 16; return restore_fast_kernel<PREC, 16, ROPE, OUT, HP>; }
     }
     *chosen = 0;
     return nullptr;
 }
 
-template <int PREC>
-FastFn pick_fast(int ks, bool rope, int out_dtype, int* chosen) {
+template <int PREC, int OUT, int HP>
+FastFn fast_rope(int ks, bool rope, int* chosen) {
+    return rope ? fast_ks<PREC, true, OUT, HP>(ks, chosen) : fast_ks<PREC, false, OUT, HP>(ks, chosen);
+}
+
+template <int PREC, int HP>
+FastFn fast_out(int ks, bool rope, int out_dtype, int* chosen) {
     switch (out_dtype) {
-        case RCH_DT_F32: return rope ? fast_ks<PREC, true, RCH_DT_F32>(ks, chosen) : fast_ks<PREC, false, RCH_DT_F32>(ks, chosen);
-        case RCH_DT_F16: return rope ? fast_ks<PREC, true, RCH_DT_F16>(ks, chosen) : fast_ks<PREC, false, RCH_DT_F16>(ks, chosen);
-        case RCH_DT_BF16: return rope ? fast_ks<PREC, true, RCH_DT_BF16>(ks, chosen) : fast_ks<PREC, false, RCH_DT_BF16>(ks, chosen);
+        case RCH_DT_F32: return fast_rope<PREC, RCH_DT_F32, HP>(ks, rope, chosen);
+        case RCH_DT_F16: return fast_rope<PREC, RCH_DT_F16, HP>(ks, rope, chosen);
+        case RCH_DT_BF16: return fast_rope<PREC, RCH_DT_BF16, HP>(ks, rope, chosen);
         default: *chosen = 0; return nullptr;
     }
+}
+
+template <int PREC>
+FastFn pick_fast(int ks, bool rope, int out_dtype, bool head_pairs, int* chosen) {
+    return head_pairs ? fast_out<PREC, 2>(ks, rope, out_dtype, chosen) : fast_out<PREC, 1>(ks, rope, out_dtype, chosen);
 }
 
 }  // namespace
 
 // One per precision translation unit (restore_<precision>.hip); nullptr when no fast variant
-// covers the rank.
-FastFn pick_fast_fp16(int ks, bool rope, int out_dtype, int* chosen);
-FastFn pick_fast_fp16x2(int ks, bool rope, int out_dtype, int* chosen);
-FastFn pick_fast_bf16(int ks, bool rope, int out_dtype, int* chosen);
+// covers the rank (head_pairs: the two-heads-per-step variant, RCH_GF_HEAD_PAIRS).
+FastFn pick_fast_fp16(int ks, bool rope, int out_dtype, bool head_pairs, int* chosen);
+FastFn pick_fast_fp16x2(int ks, bool rope, int out_dtype, bool head_pairs, int* chosen);
+FastFn pick_fast_bf16(int ks, bool rope, int out_dtype, bool head_pairs, int* chosen);
 
 }  // namespace rch

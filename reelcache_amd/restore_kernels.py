@@ -78,7 +78,7 @@ _MATRIX_CORE_PRECISIONS = ("fp32", "fp16", "fp16x2", "bf16")
 TILE_TOKENS = 128  # tokens per workgroup tile (4 waves x 32)
 SLICE_TOKENS = 32  # tokens per tile of the channel-slice kernel (one wave's MFMA columns)
 _DEFAULT_CONFIG = {"TILE_TOKENS": TILE_TOKENS, "BLOCK_N": 32, "waves": 4, "workgroups_per_cu": None,
-                   "store_cost": 4.0, "fast_variant": True, "slice_variant": False}
+                   "store_cost": 4.0, "fast_variant": True, "slice_variant": False, "head_pairs": True}
 # Triton tile keys the reference accepts in ``config``; they have no meaning for the HIP
 # kernels and are accepted (and ignored) so that caller configurations keep working.
 _REFERENCE_TILE_KEYS = {"BLOCK_M", "BLOCK_K", "num_warps", "num_stages", "N_GROUP", "PIC_T", "UNPACK_BLOCK_K",
@@ -1366,7 +1366,8 @@ class _CallPlan:
         self.config = config
         self.keepalive = keepalive
         self.grids = []
-        self.variants = []  # per restore launch: "fast" (straight-line kernel) or "general"
+        self.variants = []  # per restore launch: "pairs" / "fast" (straight-line kernel, two or one
+        #                     heads per step), "sliced" (channel-slice kernel) or "general"
 
     # -- per-job descriptor fields ------------------------------------------------------------
     # Rows are plain lists indexed by the rch_job field columns (``_JOB_INDEX``); one int64
@@ -1537,6 +1538,7 @@ class _CallPlan:
         store_cost = float(_config_value(self.config, "store_cost"))
         launches_planned = []
         allow_slice = allow_fast and bool(_config_value(self.config, "slice_variant"))
+        allow_pairs = allow_fast and bool(_config_value(self.config, "head_pairs"))
         for key, members in groups.items():
             kind, group_flags = key[0], key[-1]
             first = jobs[members[0]]
@@ -1565,7 +1567,9 @@ class _CallPlan:
             if kind == _lib.SRC_DENSE:
                 launches_planned.append(("dense", tile_offset, len(tiles), channels, head_dim, out_dtype))
                 continue
-            blocks_per_tile = (channels + 31) // 32
+            if allow_pairs and group_flags & _lib.GF_FAST and (channels // head_dim) % 2 == 0:
+                group_flags |= _lib.GF_HEAD_PAIRS  # a work unit: one dim block of two heads
+            blocks_per_tile = (channels + 31) // 32 // (2 if group_flags & _lib.GF_HEAD_PAIRS else 1)
             steps = np.array([job_steps[i] for i in tiles[:, 0].tolist()], dtype=np.float64)
             per_cu = self.config.get("workgroups_per_cu") or _occupancy(self.code, kind, max_ksteps, head_dim, out_dtype,
                                                                         group_flags)
@@ -1574,7 +1578,8 @@ class _CallPlan:
             launches_planned.append(("restore", tile_offset, len(tiles), arena.add(bounds), grid, channels, head_dim,
                                      kind, out_dtype, max_ksteps, group_flags))
             self.grids.append(grid)
-            self.variants.append("fast" if group_flags & _lib.GF_FAST else "general")
+            self.variants.append("general" if not group_flags & _lib.GF_FAST
+                                 else ("pairs" if group_flags & _lib.GF_HEAD_PAIRS else "fast"))
         bound_tiles = _tiles(bound_jobs, jobs) if bound_jobs else None
         bound_tile_offset = arena.add(bound_tiles) if bound_jobs else None
         pack_desc = np.zeros(n_packs, dtype=_lib.PACK_DTYPE)

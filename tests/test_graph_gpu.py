@@ -1,7 +1,7 @@
 """GPU test of restores captured in a HIP graph.
 
-A call of K (RoPE) and V jobs is captured once per kernel variant (straight-line, channel-slice,
-general); the graph is replayed several times, with eager work and synchronizations between the
+A call of K (RoPE) and V jobs is captured once per kernel variant (straight-line with two or one
+heads per step, channel-slice, general); the graph is replayed several times, with eager work and synchronizations between the
 replays and the destinations overwritten before each, and every replay must reproduce the eager
 result bit for bit.  Captured calls take their descriptor staging from memory reserved
 beforehand (``reserve_capture_staging``); the capture itself allocates no pinned memory and
@@ -37,7 +37,7 @@ def _jobs(device):
     return jobs, (cache_k, cache_v)
 
 
-@pytest.mark.parametrize("config", [{}, {"slice_variant": True}, {"fast_variant": False}])
+@pytest.mark.parametrize("config", [{}, {"head_pairs": False}, {"slice_variant": True}, {"fast_variant": False}])
 def test_captured_restore_replays_match_eager(device, config):
     jobs, caches = _jobs(device)
     for cache in caches:

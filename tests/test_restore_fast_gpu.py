@@ -2,7 +2,8 @@
 csrc/restore_slice.h).
 
 Launch groups whose jobs all qualify (uint8 codes in 16-byte aligned rows or pictures,
-head_dim % 32 == 0, unit-stride aligned destinations) run the straight-line kernel, or, with
+head_dim % 32 == 0, unit-stride aligned destinations) run the straight-line kernel (two heads
+per step when the head count is even, one with ``config={"head_pairs": False}``), or, with
 ``config={"slice_variant": True}``, the channel-slice kernel (uint8 rows); every case here runs
 the same inputs through the straight-line, channel-slice and general kernels
 (``config={"fast_variant": False}``) and requires equal values, then checks them against the
@@ -32,7 +33,8 @@ SHAPES = [
 ]
 
 
-VARIANTS = {"sliced": {"slice_variant": True}, "fast": {}, "general": {"fast_variant": False}}
+VARIANTS = {"sliced": {"slice_variant": True}, "pairs": {}, "fast": {"head_pairs": False},
+            "general": {"fast_variant": False}}
 
 
 def _copies(seed, precision, out_dtype, shape, device, count=len(VARIANTS)):
@@ -65,9 +67,10 @@ def test_fast_matches_general_and_oracle(device, precision, out_dtype):
         seed = zlib.crc32(f"{precision}/{out_dtype}/{index}".encode())
         cases = dict(zip(VARIANTS, _copies(seed, precision, out_dtype, shape, device)))
         for variant, case in cases.items():
-            assert _run(case, precision, variant) == [variant], shape
+            label = "fast" if variant == "pairs" and shape[1] % 2 else variant  # odd heads: one per step
+            assert _run(case, precision, variant) == [label], shape
         out_general = written(cases["general"])
-        for variant in ("sliced", "fast"):
+        for variant in ("sliced", "pairs", "fast"):
             assert np.array_equal(written(cases[variant]), out_general), f"{shape}: {variant} and general kernels differ"
         _check_bound(cases["sliced"], precision)
         # Tokens outside the slot are untouched.
@@ -81,8 +84,9 @@ def test_fast_matches_general_and_oracle(device, precision, out_dtype):
 
 def test_fast_pictures_and_mixed_groups(device):
     """Pictures and uint8 sources, K (RoPE) and V (none) jobs in one call: the call splits into
-    one straight-line launch per (source kind, RoPE) group; with the channel-slice variant
-    enabled, the uint8 rows take it and the pictures stay on the straight-line kernel."""
+    one straight-line launch per (source kind, RoPE) group (two heads per step: the head count
+    is even); with the channel-slice variant enabled, the uint8 rows take it and the pictures
+    stay on the straight-line kernel."""
     rng = np.random.default_rng(31)
     table = rk.RopeTable.from_complex(torch.from_numpy(orc.wan_freqs(64, 64)))
     heads, head_dim, grid, tokens = 4, 64, (2, 12, 14), 336
@@ -98,12 +102,12 @@ def test_fast_pictures_and_mixed_groups(device):
                                out_dtype="bfloat16", device=device))
     handle = rk.reconstruct([case.job for case in cases])
     handle.release()
-    assert sorted(handle.stats["variants"]) == ["fast", "fast"]
+    assert sorted(handle.stats["variants"]) == ["pairs", "pairs"]
     for case in cases:
         _check_bound(case, "fp16x2")
     handle = rk.reconstruct([case.job for case in cases], config={"slice_variant": True})
     handle.release()
-    assert sorted(handle.stats["variants"]) == ["fast", "sliced"]
+    assert sorted(handle.stats["variants"]) == ["pairs", "sliced"]
     for case in cases:
         _check_bound(case, "fp16x2")
 
