@@ -67,7 +67,10 @@ extern "C" {
                               stride; the group: head_dim % 32 == 0, channels == heads * head_dim */
 #define RCH_GF_ROPE 2      /* with RCH_GF_FAST: every job of the group has RoPE (otherwise none has) */
 #define RCH_GF_HEAD_PAIRS 4 /* with RCH_GF_FAST and an even head count: each work unit covers one
-                               32-channel dim block of two adjacent heads (see rch_restore) */
+                               32-channel dim block of two adjacent heads (see rch_restore); only
+                               for max_ksteps <= 12 (RCH_E_CONFIG otherwise).  Straight-line
+                               variants cover max_ksteps <= 12 (fp16x2) or 16 (fp16, bf16); larger
+                               ranks run the general kernel whatever the flags. */
 
 /*
  * One reconstruction job: one restored [N, C] matrix written into one native

@@ -57,12 +57,19 @@ __global__ void __launch_bounds__(256) basis_pack_kernel(const rch_pack* __restr
     __shared__ float block_max[4][2];
     __shared__ int block_exp[2];
     if (scaled) {
+        // Rows are read four at a time so their loads are in flight together; rows past the rank
+        // re-read the last row (a duplicate does not change the maximum).
+        constexpr int kRows = 4;
         float m = 0.0f;
-        for (int64_t r = row_lane; r < P.rank; r += 32) {
-            float v[8];
-            basis_row8(P, dtype, vec, r, c_base + 8 * chunk, v);
+        for (int64_t r0 = row_lane; r0 < P.rank; r0 += 32 * kRows) {
+            float v[kRows][8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[j]));
+            for (int u = 0; u < kRows; ++u) basis_row8(P, dtype, vec, min(r0 + 32 * u, P.rank - 1), c_base + 8 * chunk, v[u]);
+#pragma unroll
+            for (int u = 0; u < kRows; ++u) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[u][j]));
+            }
         }
         // Block of this thread: chunk / 4.  Reduce over chunk bits 0-1 and the 8 row lanes of the wave.
         m = fmaxf(m, __shfl_xor(m, 1));
@@ -252,6 +259,9 @@ static int pick_launch(int precision, int source_kind, int max_ksteps, int head_
             return RCH_OK;
         }
     }
+    // Head-pair work units exist only in the straight-line kernel.
+    if (group_flags & RCH_GF_HEAD_PAIRS)
+        return fail(RCH_E_CONFIG, "RCH_GF_HEAD_PAIRS: no straight-line variant covers %d rank steps here", max_ksteps);
     RestoreVariant variant;
     switch (precision) {
         case RCH_PREC_FP32: variant = pick_restore_fp32(source_kind, max_ksteps); break;

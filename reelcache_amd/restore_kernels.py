@@ -1326,6 +1326,10 @@ def _occupancy(code, kind, max_ksteps, head_dim, out_dtype, group_flags):
 
 
 _FAST_LIMIT = 2 ** 31
+# Largest ceil(rank / 16) the compiled straight-line variants cover (csrc/restore_fast.h: fast_ks);
+# larger ranks run the general kernel.
+_FAST_MAX_KSTEPS = {"fp16x2": 12, "fp16": 16, "bf16": 16, "fp32": 0}
+_PAIRS_MAX_KSTEPS = 12
 
 
 def _fast_flags(row, job, precision):
@@ -1567,7 +1571,10 @@ class _CallPlan:
             if kind == _lib.SRC_DENSE:
                 launches_planned.append(("dense", tile_offset, len(tiles), channels, head_dim, out_dtype))
                 continue
-            if allow_pairs and group_flags & _lib.GF_FAST and (channels // head_dim) % 2 == 0:
+            if group_flags & _lib.GF_FAST and max_ksteps > _FAST_MAX_KSTEPS[precision]:
+                group_flags = 0  # no straight-line variant holds this many rank steps in registers
+            if (allow_pairs and group_flags & _lib.GF_FAST and (channels // head_dim) % 2 == 0
+                    and max_ksteps <= _PAIRS_MAX_KSTEPS):
                 group_flags |= _lib.GF_HEAD_PAIRS  # a work unit: one dim block of two heads
             blocks_per_tile = (channels + 31) // 32 // (2 if group_flags & _lib.GF_HEAD_PAIRS else 1)
             steps = np.array([job_steps[i] for i in tiles[:, 0].tolist()], dtype=np.float64)

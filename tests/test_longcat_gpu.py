@@ -1,0 +1,56 @@
+"""GPU parity at the LongCat layer shape: 32 heads x 128 (4096 channels),
+LongCat's [B, H, T, D] cache layout, 4680-token chunks with high per-chunk ranks (256-512 of one
+512-row bf16 basis per K/V target), no RoPE (LongCat stores pre-RoPE K,
+reelcache/restore_kernels.py:504-506).
+
+Three chunks per target keep the oracle affordable; the checks are
+  * every element of every slot is written (no fill value left) and the tokens around the slots
+    are untouched;
+  * sampled token rows of every job against the oracle's elementwise error bound
+    (reelcache/restore_kernels.py:1208-1227).
+Ranks above 192 (fp16x2) have no straight-line variant, so these groups run the general kernel.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from reelcache_amd import restore_kernels as rk
+from oracle import restore as orc
+
+from restore_cases import destination, make_case, orthonormal_basis
+
+pytestmark = pytest.mark.gpu
+
+HEADS, HEAD_DIM, GRID = 32, 128, (3, 30, 52)
+RANKS = (512, 384, 256)
+FILL = -123.0
+
+
+def test_longcat_shape_restore(device):
+    rng = np.random.default_rng(91)
+    tokens = int(np.prod(GRID))
+    history = len(RANKS) * tokens
+    cases, caches = [], []
+    for target in range(2):  # K, V
+        cache = destination("BHTD", history, HEADS, HEAD_DIM, "bfloat16", device, offset=7, extra=5, fill=FILL)
+        basis = orthonormal_basis(512, HEADS * HEAD_DIM, rng, torch.bfloat16).to(device)
+        caches.append(cache)
+        for chunk, rank in enumerate(RANKS if target == 0 else RANKS[::-1]):
+            view = rk.NativeView(cache, "BHTD", token_offset=7 + chunk * tokens)
+            cases.append(make_case(rng, grid=GRID, heads=HEADS, head_dim=HEAD_DIM, rank=rank, rope="none",
+                                   view=view, basis=basis, out_dtype="bfloat16", device=device))
+    handle = rk.reconstruct([case.job for case in cases])
+    handle.release()
+    assert handle.stats["variants"] and set(handle.stats["variants"]) == {"general"}, handle.stats["variants"]
+    for cache in caches:
+        tokens_major = cache[0].transpose(0, 1)  # [T, H, D]
+        assert not bool((tokens_major[7:7 + history] == FILL).any()), "a slot element was not written"
+        assert bool((tokens_major[:7] == FILL).all()) and bool((tokens_major[7 + history:] == FILL).all())
+    for case in cases:
+        rows = np.unique(np.concatenate(([0, tokens - 1], rng.choice(tokens, 30, replace=False))))
+        values, bound = orc.error_bound(case.coefficients[rows], case.basis, HEADS, None, "fp16x2", "bfloat16")
+        got = case.job.destination.slot(tokens)  # [N, H, D] view of the slot
+        got = got[torch.from_numpy(rows).to(got.device)].reshape(len(rows), -1).double().cpu().numpy()
+        excess = np.abs(got - values) - bound
+        assert float(excess.max()) <= 0, f"{int((excess > 0).sum())} elements exceed the error bound"
