@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-#define RCH_ABI_VERSION 5
+#define RCH_ABI_VERSION 6
 
 /* Status codes (mapped to reelcache errors by the host). */
 #define RCH_OK 0
@@ -71,6 +71,11 @@ extern "C" {
                                for max_ksteps <= 12 (RCH_E_CONFIG otherwise).  Straight-line
                                variants cover max_ksteps <= 12 (fp16x2) or 16 (fp16, bf16); larger
                                ranks run the general kernel whatever the flags. */
+#define RCH_GF_SPLIT_RANK 8 /* with RCH_GF_FAST, uint8 code rows, not with RCH_GF_HEAD_PAIRS: the
+                               straight-line kernel with 8-wave workgroups that split the rank
+                               steps in two halves (max_ksteps up to 32); work units as without
+                               flags.  Its fp32 sums add the halves' partial sums, so its output
+                               may differ from the one-chain kernels in the last bit. */
 
 /*
  * One reconstruction job: one restored [N, C] matrix written into one native

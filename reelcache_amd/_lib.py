@@ -16,7 +16,7 @@ import numpy as np
 from .errors import ConfigurationError, UnsupportedError
 
 LIBRARY = Path(__file__).resolve().with_name("libreelcache_hip.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # Status codes (RCH_E_*).
 OK, E_CONFIG, E_UNSUPPORTED, E_LAUNCH = 0, 1, 2, 3
@@ -27,7 +27,7 @@ DT_F32, DT_F16, DT_BF16, DT_U8, DT_F64 = 0, 1, 2, 3, 4
 SRC_FLOAT, SRC_U8, SRC_PICTURE, SRC_DENSE = 0, 1, 2, 3
 ROPE_NONE, ROPE_SEPARABLE, ROPE_DENSE = 0, 1, 2
 JF_SRC_VEC, JF_DST_VEC, JF_ROPE_VEC = 1, 2, 4
-GF_FAST, GF_ROPE, GF_HEAD_PAIRS = 1, 2, 4
+GF_FAST, GF_ROPE, GF_HEAD_PAIRS, GF_SPLIT_RANK = 1, 2, 4, 8
 
 # rch_job field order (40 x int64).
 JOB_FIELDS = (

@@ -238,6 +238,7 @@ struct Launch {
     bool fast;
     int ks;
     bool chunked;
+    int threads;  // workgroup size
 };
 
 static int pick_launch(int precision, int source_kind, int max_ksteps, int head_dim, int out_dtype, int group_flags,
@@ -245,23 +246,29 @@ static int pick_launch(int precision, int source_kind, int max_ksteps, int head_
     if ((group_flags & RCH_GF_FAST) && head_dim % 32 == 0 &&
         (source_kind == RCH_SRC_U8 || source_kind == RCH_SRC_PICTURE)) {
         const bool rope = (group_flags & RCH_GF_ROPE) != 0;
-        const bool pairs = (group_flags & RCH_GF_HEAD_PAIRS) != 0;
+        if ((group_flags & RCH_GF_HEAD_PAIRS) && (group_flags & RCH_GF_SPLIT_RANK))
+            return fail(RCH_E_CONFIG, "RCH_GF_HEAD_PAIRS and RCH_GF_SPLIT_RANK exclude each other");
+        if ((group_flags & RCH_GF_SPLIT_RANK) && source_kind != RCH_SRC_U8)
+            return fail(RCH_E_CONFIG, "RCH_GF_SPLIT_RANK takes uint8 code rows only");
+        const int shape = (group_flags & RCH_GF_SPLIT_RANK) ? kRankHalves
+                          : ((group_flags & RCH_GF_HEAD_PAIRS) ? kHeadPairs : kOneHead);
         FastFn fn = nullptr;
         int ks = 0;
         switch (precision) {
-            case RCH_PREC_FP16: fn = pick_fast_fp16(max_ksteps, rope, out_dtype, pairs, &ks); break;
-            case RCH_PREC_FP16X2: fn = pick_fast_fp16x2(max_ksteps, rope, out_dtype, pairs, &ks); break;
-            case RCH_PREC_BF16: fn = pick_fast_bf16(max_ksteps, rope, out_dtype, pairs, &ks); break;
+            case RCH_PREC_FP16: fn = pick_fast_fp16(max_ksteps, rope, out_dtype, shape, &ks); break;
+            case RCH_PREC_FP16X2: fn = pick_fast_fp16x2(max_ksteps, rope, out_dtype, shape, &ks); break;
+            case RCH_PREC_BF16: fn = pick_fast_bf16(max_ksteps, rope, out_dtype, shape, &ks); break;
             default: break;
         }
         if (fn) {
-            *out = {reinterpret_cast<const void*>(fn), true, ks, false};
+            *out = {reinterpret_cast<const void*>(fn), true, ks, false, shape == kRankHalves ? 2 * kThreads : kThreads};
             return RCH_OK;
         }
     }
-    // Head-pair work units exist only in the straight-line kernel.
-    if (group_flags & RCH_GF_HEAD_PAIRS)
-        return fail(RCH_E_CONFIG, "RCH_GF_HEAD_PAIRS: no straight-line variant covers %d rank steps here", max_ksteps);
+    // Head-pair work units and rank halves exist only in the straight-line kernel.
+    if (group_flags & (RCH_GF_HEAD_PAIRS | RCH_GF_SPLIT_RANK))
+        return fail(RCH_E_CONFIG, "RCH_GF_HEAD_PAIRS / RCH_GF_SPLIT_RANK: no straight-line variant covers %d rank "
+                    "steps here", max_ksteps);
     RestoreVariant variant;
     switch (precision) {
         case RCH_PREC_FP32: variant = pick_restore_fp32(source_kind, max_ksteps); break;
@@ -271,7 +278,7 @@ static int pick_launch(int precision, int source_kind, int max_ksteps, int head_
         default: return fail(RCH_E_UNSUPPORTED, "precision %d has no matrix-core path on gfx950", precision);
     }
     if (!variant.fn) return fail(RCH_E_CONFIG, "source kind %d is not a coefficient source", source_kind);
-    *out = {reinterpret_cast<const void*>(variant.fn), false, variant.ks, variant.chunked};
+    *out = {reinterpret_cast<const void*>(variant.fn), false, variant.ks, variant.chunked, kThreads};
     return RCH_OK;
 }
 
@@ -283,7 +290,7 @@ int rch_restore_occupancy(int precision, int source_kind, int max_ksteps, int he
     const int status = pick_launch(precision, source_kind, max_ksteps, head_dim, out_dtype, group_flags, &launch);
     if (status) return status;
     int blocks = 0;
-    const hipError_t error = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, launch.fn, kThreads, 0);
+    const hipError_t error = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, launch.fn, launch.threads, 0);
     if (error != hipSuccess)
         return fail(RCH_E_LAUNCH, "rch_restore_occupancy: %s", hipGetErrorString(error));
     *blocks_per_cu = blocks;
@@ -307,8 +314,8 @@ int rch_restore(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev, i
     if (status) return status;
     if (launch.fast) {
         hipLaunchKernelGGL(reinterpret_cast<FastFn>(const_cast<void*>(launch.fn)), dim3(static_cast<unsigned>(grid)),
-                           dim3(kThreads), 0, as_stream(stream), jobs_dev, tiles_dev, bounds_dev, scratch_dev,
-                           channels / head_dim, head_dim);
+                           dim3(static_cast<unsigned>(launch.threads)), 0, as_stream(stream), jobs_dev, tiles_dev,
+                           bounds_dev, scratch_dev, channels / head_dim, head_dim);
     } else {
         const int nk = launch.chunked ? (max_ksteps + launch.ks - 1) / launch.ks : 1;
         hipLaunchKernelGGL(reinterpret_cast<RestoreFn>(const_cast<void*>(launch.fn)), dim3(static_cast<unsigned>(grid)),

@@ -41,24 +41,37 @@ constexpr int kFastOccupancy = HP == 2 ? 2 : (((KS <= 12 && !ROPE) || (KS <= 8 &
 // HP = heads per step: 1, or 2 (RCH_GF_HEAD_PAIRS, an even head count): a step then computes the
 // same 32-channel dim block of two adjacent heads, so the per-step bookkeeping, barrier and
 // waits are shared by twice the matrix work and each RoPE pair set serves both heads.
-template <int PREC, int KS, bool ROPE, int OUT, int HP>
-__global__ void __launch_bounds__(kThreads, (kFastOccupancy<KS, ROPE, HP>))
+// SPLIT = rank halves: 1, or 2 (RCH_GF_SPLIT_RANK, ranks beyond one wave's registers): the
+// workgroup has 8 waves, waves w and w + 4 hold the coefficient fragments of the same 32 tokens
+// for the low and the high half of the rank steps, each computes its half of every block's
+// product, and the high half hands its fp32 partial sums to the low half through LDS, which
+// adds them and runs the epilogue (the only difference from one chain: the fp32 summation
+// order of the two halves).
+template <int PREC, int KS, bool ROPE, int OUT, int HP, int SPLIT>
+__global__ void __launch_bounds__(kThreads * SPLIT, (SPLIT == 2 ? 1 : kFastOccupancy<KS, ROPE, HP>))
 restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict__ tiles,
                     const int32_t* __restrict__ bounds, const int32_t* __restrict__ scratch, int heads,
                     int head_dim) {
     static_assert(PREC != RCH_PREC_FP32, "the fp32 mode runs restore_kernel");
     static_assert(HP == 1 || HP == 2, "one or two heads per step");
+    static_assert(SPLIT == 1 || (SPLIT == 2 && HP == 1 && KS % 8 == 0), "rank halves: one head per step");
+    constexpr int kThreadsT = kThreads * SPLIT;          // threads of the workgroup
+    constexpr int kKsWave = KS / SPLIT;                  // rank steps held by one wave
     constexpr int kStepFrags = 64;                       // u4 fragments of one 16-rank step of one block
     constexpr int kHeadFrags = KS * kStepFrags;          // fragments of one block (one head)
     constexpr int kBuffer = HP * kHeadFrags;
-    constexpr int kPer = kBuffer / kThreads;
-    static_assert(kBuffer % kThreads == 0, "KS must be a multiple of 4: every thread moves whole fragments");
+    constexpr int kPer = kBuffer / kThreadsT;
+    static_assert(kBuffer % kThreadsT == 0, "KS must be a multiple of 4: every thread moves whole fragments");
     constexpr int kRanks = KS * 16;
     constexpr int kPitch = kRanks + 8;
     constexpr bool kFp16 = PREC == RCH_PREC_FP16 || PREC == RCH_PREC_FP16X2;
     constexpr int kEsize = OUT == RCH_DT_F32 ? 4 : 2;
+    // Rank halves: the high half's partial sums of a step, [step parity][token group][16][64 lanes]
+    // fp32, share the codes buffer (codes are read only between the barriers of a tile entry).
+    constexpr int kReduceBytes = SPLIT == 2 ? 2 * 4 * 16 * 64 * 4 : 0;
+    constexpr int kCodesBytes = kTileTokens * kPitch > kReduceBytes ? kTileTokens * kPitch : kReduceBytes;
     __shared__ u4 lds[2][kBuffer];
-    __shared__ __attribute__((aligned(16))) uint8_t codes[kTileTokens * kPitch];
+    __shared__ __attribute__((aligned(16))) uint8_t codes[kCodesBytes];
     __shared__ __attribute__((aligned(16))) float affine[2 * kRanks];
     __shared__ int block_exp[kFastMaxBlocks];  // basis block exponents of the current tile's job
 
@@ -72,7 +85,9 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
     const int last_tile = (first_unit + steps - 1) / per_tile;
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63, h = lane >> 5, col = lane & 31;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, h = lane >> 5, col = lane & 31;
+    const int group = wave & 3;      // token group: tokens 32 group .. 32 group + 31 of the tile
+    const int half = wave >> 2;      // rank half (SPLIT == 2), else 0
 
     // Unit u of a tile is (dim block u / head_steps, first head HP * (u % head_steps)).  Prefetch
     // cursors past the range end stay on the range's last tile (their fragments are fetched and
@@ -104,7 +119,7 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
             pack = make_rsrc(J->pack_ptr, int64_t(ks) * nblocks * 1024);
 #pragma unroll
             for (int i = 0; i < kPer; ++i) {
-                const int q = tid + i * kThreads;
+                const int q = tid + i * kThreadsT;
                 const int j = q / kHeadFrags, s = (q % kHeadFrags) >> 6, li = q & 63;
                 fetch_lane[i] = s < ks ? static_cast<uint32_t>(s * nblocks + j * head_blocks) * 1024u + li * 16
                                        : kOutOfRange;
@@ -118,7 +133,7 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
     };
     auto commit = [&](int buffer, const u4 (&from)[kPer]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) lds[buffer][tid + i * kThreads] = from[i];
+        for (int i = 0; i < kPer; ++i) lds[buffer][tid + i * kThreadsT] = from[i];
     };
 
     // Per-lane state of the current tile.
@@ -126,7 +141,7 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
     uint32_t row_t = 0, row_h = 0, row_w = 0;  // byte offsets of this token's RoPE rows
     __amdgpu_buffer_rsrc_t dst = make_rsrc(0, 0), pairs = make_rsrc(0, 0);
     int coef_exp = 0, sec0 = 0, sec1 = 0, head_bytes = 0;
-    CoefFrag<PREC> cf[KS];
+    CoefFrag<PREC> cf[kKsWave];
 
     f4 rope_next[4], rope_now[4];  // RoPE pairs of the next / current dim block
 
@@ -166,10 +181,13 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
     };
 
     // Tile entry: stage the tile's codes and affine in LDS, convert this wave's 32 tokens to
-    // coefficient fragments.  All waves passed a barrier since they last read codes / affine.
+    // coefficient fragments.  All waves passed a barrier since they last read codes / affine
+    // (rank halves: the low half reads partial sums and block exponents after the step barrier,
+    // so the entry starts with a barrier of its own).
     auto enter = [&](const rch_job* J, int t0, int first_bp) __attribute__((always_inline)) {
+        if constexpr (SPLIT == 2) __syncthreads();
         const int64_t tokens = J->tokens;
-        const int64_t t = t0 + wave * 32 + col;
+        const int64_t t = t0 + group * 32 + col;
         const bool valid = t < tokens;
         const Coords xy = coords(J, valid ? static_cast<int>(t) : 0);
         dst = make_rsrc(J->dst_ptr, J->dst_bytes);
@@ -195,16 +213,16 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
         head_bytes = static_cast<int>(J->dst_head_stride) * kEsize;
         const float pre = pow2f(coef_exp);  // folded into the staged affine
         const int rank = static_cast<int>(J->rank);
-        for (int i = tid; i < heads * head_blocks; i += kThreads) block_exp[i] = scratch[J->basis_exp_index + i];
-        if (J->pic_slots == 0) {  // uint8 rows, 16-byte aligned
+        for (int i = tid; i < heads * head_blocks; i += kThreadsT) block_exp[i] = scratch[J->basis_exp_index + i];
+        if (SPLIT == 2 || J->pic_slots == 0) {  // uint8 rows, 16-byte aligned (rank halves: uint8 rows only)
             const int64_t rs = J->src_row_stride;
             constexpr int kGroups = kRanks / 16;
-            constexpr int kIters = (kTileTokens * kGroups + kThreads - 1) / kThreads;
+            constexpr int kIters = (kTileTokens * kGroups + kThreadsT - 1) / kThreadsT;
             const __amdgpu_buffer_rsrc_t src = make_rsrc(J->src_ptr + t0 * rs, (tokens - t0) * rs);
             u4 bytes[kIters];
 #pragma unroll
             for (int i = 0; i < kIters; ++i) {
-                const int q = tid + i * kThreads;
+                const int q = tid + i * kThreadsT;
                 const int token = q / kGroups, g = q - token * kGroups;
                 const uint32_t offset = (q < kTileTokens * kGroups && 16 * g < rank)
                                             ? static_cast<uint32_t>(token * rs + 16 * g)
@@ -213,7 +231,7 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
             }
 #pragma unroll
             for (int i = 0; i < kIters; ++i) {
-                const int q = tid + i * kThreads;
+                const int q = tid + i * kThreadsT;
                 const int token = q / kGroups, g = q - token * kGroups;
                 if (q < kTileTokens * kGroups) {
                     // Bytes past the rank (row padding) are staged as they are: their affine
@@ -242,15 +260,15 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
                     if (base + 2 * i < kRanks) row[base + 2 * i] = got[i];
             }
         }
-        for (int i = tid; i < kRanks; i += kThreads) {
+        for (int i = tid; i < kRanks; i += kThreadsT) {
             affine[i] = i < rank ? __fmul_rn(gin<float>(J->scale_ptr)[i], pre) : 0.0f;
             affine[kRanks + i] = i < rank ? __fmul_rn(gin<float>(J->offset_ptr)[i], pre) : 0.0f;
         }
         __syncthreads();
-        const uint8_t* mine = codes + (wave * 32 + col) * kPitch;
+        const uint8_t* mine = codes + (group * 32 + col) * kPitch;
 #pragma unroll
-        for (int s = 0; s < KS; ++s) {
-            const int kl = 16 * s + 8 * h;
+        for (int s = 0; s < kKsWave; ++s) {
+            const int kl = 16 * (half * kKsWave + s) + 8 * h;
             const u2 b = *reinterpret_cast<const u2*>(mine + kl);
             const f4 sc0 = *reinterpret_cast<const f4*>(affine + kl);
             const f4 sc1 = *reinterpret_cast<const f4*>(affine + kl + 4);
@@ -266,14 +284,58 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
             }
             set_frag_scaled(cf[s], a);
         }
+        if constexpr (SPLIT == 2) __syncthreads();  // codes are read; the steps reuse them for partial sums
     };
 
-    // One step: product of the staged block, scale, RoPE, cast, store.
+    // Epilogue of head x of a step: undo the exponents, RoPE, cast, store this lane's 16 channels.
+    auto epilogue = [&](const Cursor& c, int x, const f16v& acc, const f4 (&rope)[4]) __attribute__((always_inline)) {
+        // Undo the coefficient prescale and the block's basis exponent (exact powers of two).
+        const int e = coef_exp + block_exp[(c.head + x) * head_blocks + c.bp];
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = __builtin_amdgcn_ldexpf(acc[i], -e);
+        if constexpr (ROPE) {
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                rotate(v[4 * p], v[4 * p + 1], rope[p][0], rope[p][1]);
+                rotate(v[4 * p + 2], v[4 * p + 3], rope[p][2], rope[p][3]);
+            }
+        }
+        const uint32_t at = dst_lane + static_cast<uint32_t>((c.head + x) * head_bytes + c.bp * 32 * kEsize);
+        if constexpr (OUT == RCH_DT_F32) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const f4 out = {v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, out), dst, at + 16 * q, 0, 0);
+            }
+        } else if constexpr (OUT == RCH_DT_BF16) {
+            bf8 a, b;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                a[i] = static_cast<__bf16>(v[i]);
+                b[i] = static_cast<__bf16>(v[i + 8]);
+            }
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, a), dst, at, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, b), dst, at + 16, 0, 0);
+        } else {
+            h8 a, b;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                a[i] = static_cast<_Float16>(v[i]);
+                b[i] = static_cast<_Float16>(v[i + 8]);
+            }
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, a), dst, at, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, b), dst, at + 16, 0, 0);
+        }
+    };
+
+    // One step: products of the staged block(s) over this wave's rank steps, then the epilogue;
+    // ends with the step barrier (after which the LDS buffer of this step may be refilled).
     auto finish = [&](const Cursor& c, int buffer, const f4 (&rope)[4]) __attribute__((always_inline)) {
         // Basis fragments are read from LDS three steps ahead of their products (a rotating
         // window of four registers per head).
-        constexpr int kAhead = 3;
-        const u4* frags = &lds[buffer][lane];
+        constexpr int kAhead = kKsWave < 3 ? kKsWave : 3;
+        const u4* frags = &lds[buffer][lane] + half * kKsWave * kStepFrags;
         u4 window[HP][kAhead + 1];
 #pragma unroll
         for (int j = 0; j < kAhead; ++j) {
@@ -284,53 +346,31 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
 #pragma unroll
         for (int x = 0; x < HP; ++x) acc[x] = f16v{};
 #pragma unroll
-        for (int s = 0; s < KS; ++s) {
+        for (int s = 0; s < kKsWave; ++s) {
 #pragma unroll
             for (int x = 0; x < HP; ++x) {
-                if (s + kAhead < KS) window[x][(s + kAhead) % (kAhead + 1)] = frags[x * kHeadFrags + (s + kAhead) * kStepFrags];
+                if (s + kAhead < kKsWave) window[x][(s + kAhead) % (kAhead + 1)] = frags[x * kHeadFrags + (s + kAhead) * kStepFrags];
                 acc[x] = mfma_frag<PREC>(window[x][s % (kAhead + 1)], cf[s], acc[x]);
             }
         }
-        const uint32_t offset = dst_lane + static_cast<uint32_t>(c.head * head_bytes + c.bp * 32 * kEsize);
+        if constexpr (SPLIT == 1) {
 #pragma unroll
-        for (int x = 0; x < HP; ++x) {
-            // Undo the coefficient prescale and the block's basis exponent (exact powers of two).
-            const int e = coef_exp + block_exp[(c.head + x) * head_blocks + c.bp];
-            float v[16];
+            for (int x = 0; x < HP; ++x) epilogue(c, x, acc[x], rope);
+            __syncthreads();
+        } else {
+            // Partial sums of the high half, lane-contiguous per accumulator element (one
+            // 4-byte LDS word per lane and element: no bank conflicts).
+            float* partial = reinterpret_cast<float*>(codes) + ((buffer * 4 + group) * 16) * 64 + lane;
+            if (half == 1) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = __builtin_amdgcn_ldexpf(acc[x][i], -e);
-            if constexpr (ROPE) {
-#pragma unroll
-                for (int p = 0; p < 4; ++p) {
-                    rotate(v[4 * p], v[4 * p + 1], rope[p][0], rope[p][1]);
-                    rotate(v[4 * p + 2], v[4 * p + 3], rope[p][2], rope[p][3]);
-                }
+                for (int i = 0; i < 16; ++i) partial[i * 64] = acc[0][i];
             }
-            const uint32_t at = offset + static_cast<uint32_t>(x * head_bytes);
-            if constexpr (OUT == RCH_DT_F32) {
+            __syncthreads();
+            if (half == 0) {
+                f16v sum = acc[0];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const f4 out = {v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
-                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, out), dst, at + 16 * q, 0, 0);
-                }
-            } else if constexpr (OUT == RCH_DT_BF16) {
-                bf8 a, b;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    a[i] = static_cast<__bf16>(v[i]);
-                    b[i] = static_cast<__bf16>(v[i + 8]);
-                }
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, a), dst, at, 0, 0);
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, b), dst, at + 16, 0, 0);
-            } else {
-                h8 a, b;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    a[i] = static_cast<_Float16>(v[i]);
-                    b[i] = static_cast<_Float16>(v[i + 8]);
-                }
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, a), dst, at, 0, 0);
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, b), dst, at + 16, 0, 0);
+                for (int i = 0; i < 16; ++i) sum[i] += partial[i * 64];
+                epilogue(c, 0, sum, rope);
             }
         }
     };
@@ -372,8 +412,7 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
             for (int i = 0; i < run; ++i, ++st) {
                 commit((st + 1) & 1, ring);
                 fetch(ahead2, ring);
-                finish(now, st & 1, rope_now);
-                __syncthreads();
+                finish(now, st & 1, rope_now);  // ends with the step barrier
                 if constexpr (ROPE) {
                     if (i + 1 == run) {
 #pragma unroll
@@ -390,44 +429,64 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
 
 typedef void (*FastFn)(const rch_job*, const int32_t*, const int32_t*, const int32_t*, int, int);
 
+// Work-unit shape of a straight-line launch.
+enum FastShape : int { kOneHead = 0, kHeadPairs = 1, kRankHalves = 2 };
+
 template <int PREC, bool ROPE, int OUT, int HP>
 FastFn fast_ks(int ks, int* chosen) {
-    if (ks <= 4) { *chosen = 4; return restore_fast_kernel<PREC, 4, ROPE, OUT, HP>; }
-    if (ks <= 8) { *chosen = 8; return restore_fast_kernel<PREC, 8, ROPE, OUT, HP>; }
-    if (ks <= 12) { *chosen = 12; return restore_fast_kernel<PREC, 12, ROPE, OUT, HP>; }
+    if (ks <= 4) { *chosen = 4; return restore_fast_kernel<PREC, 4, ROPE, OUT, HP, 1>; }
+    if (ks <= 8) { *chosen = 8; return restore_fast_kernel<PREC, 8, ROPE, OUT, HP, 1>; }
+    if (ks <= 12) { *chosen = 12; return restore_fast_kernel<PREC, 12, ROPE, OUT, HP, 1>; }
     if constexpr (PREC != RCH_PREC_FP16X2 && HP == 1) {
-        if (ks <= 16) { *chosen = 16; return restore_fast_kernel<PREC, 16, ROPE, OUT, HP>; }
+        if (ks <= 16) { *chosen = 16; return restore_fast_kernel<PREC, 16, ROPE, OUT, HP, 1>; }
     }
     *chosen = 0;
     return nullptr;
 }
 
-template <int PREC, int OUT, int HP>
-FastFn fast_rope(int ks, bool rope, int* chosen) {
-    return rope ? fast_ks<PREC, true, OUT, HP>(ks, chosen) : fast_ks<PREC, false, OUT, HP>(ks, chosen);
+// Rank halves: the rank steps beyond the one-wave variants, up to 32 (512 ranks).
+template <int PREC, bool ROPE, int OUT>
+FastFn split_ks(int ks, int* chosen) {
+    if constexpr (PREC == RCH_PREC_FP16X2) {
+        if (ks <= 16) { *chosen = 16; return restore_fast_kernel<PREC, 16, ROPE, OUT, 1, 2>; }
+    }
+    if (ks <= 24) { *chosen = 24; return restore_fast_kernel<PREC, 24, ROPE, OUT, 1, 2>; }
+    if (ks <= 32) { *chosen = 32; return restore_fast_kernel<PREC, 32, ROPE, OUT, 1, 2>; }
+    *chosen = 0;
+    return nullptr;
 }
 
-template <int PREC, int HP>
-FastFn fast_out(int ks, bool rope, int out_dtype, int* chosen) {
-    switch (out_dtype) {
-        case RCH_DT_F32: return fast_rope<PREC, RCH_DT_F32, HP>(ks, rope, chosen);
-        case RCH_DT_F16: return fast_rope<PREC, RCH_DT_F16, HP>(ks, rope, chosen);
-        case RCH_DT_BF16: return fast_rope<PREC, RCH_DT_BF16, HP>(ks, rope, chosen);
+template <int PREC, bool ROPE, int OUT>
+FastFn fast_shape(int ks, int shape, int* chosen) {
+    switch (shape) {
+        case kOneHead: return fast_ks<PREC, ROPE, OUT, 1>(ks, chosen);
+        case kHeadPairs: return fast_ks<PREC, ROPE, OUT, 2>(ks, chosen);
+        case kRankHalves: return split_ks<PREC, ROPE, OUT>(ks, chosen);
         default: *chosen = 0; return nullptr;
     }
 }
 
+template <int PREC, int OUT>
+FastFn fast_rope(int ks, bool rope, int shape, int* chosen) {
+    return rope ? fast_shape<PREC, true, OUT>(ks, shape, chosen) : fast_shape<PREC, false, OUT>(ks, shape, chosen);
+}
+
 template <int PREC>
-FastFn pick_fast(int ks, bool rope, int out_dtype, bool head_pairs, int* chosen) {
-    return head_pairs ? fast_out<PREC, 2>(ks, rope, out_dtype, chosen) : fast_out<PREC, 1>(ks, rope, out_dtype, chosen);
+FastFn pick_fast(int ks, bool rope, int out_dtype, int shape, int* chosen) {
+    switch (out_dtype) {
+        case RCH_DT_F32: return fast_rope<PREC, RCH_DT_F32>(ks, rope, shape, chosen);
+        case RCH_DT_F16: return fast_rope<PREC, RCH_DT_F16>(ks, rope, shape, chosen);
+        case RCH_DT_BF16: return fast_rope<PREC, RCH_DT_BF16>(ks, rope, shape, chosen);
+        default: *chosen = 0; return nullptr;
+    }
 }
 
 }  // namespace
 
 // One per precision translation unit (restore_<precision>.hip); nullptr when no fast variant
-// covers the rank (head_pairs: the two-heads-per-step variant, RCH_GF_HEAD_PAIRS).
-FastFn pick_fast_fp16(int ks, bool rope, int out_dtype, bool head_pairs, int* chosen);
-FastFn pick_fast_fp16x2(int ks, bool rope, int out_dtype, bool head_pairs, int* chosen);
-FastFn pick_fast_bf16(int ks, bool rope, int out_dtype, bool head_pairs, int* chosen);
+// of that work-unit shape (FastShape) covers the rank.
+FastFn pick_fast_fp16(int ks, bool rope, int out_dtype, int shape, int* chosen);
+FastFn pick_fast_fp16x2(int ks, bool rope, int out_dtype, int shape, int* chosen);
+FastFn pick_fast_bf16(int ks, bool rope, int out_dtype, int shape, int* chosen);
 
 }  // namespace rch

@@ -5,8 +5,8 @@ namespace rch {
 
 RestoreVariant pick_restore_fp16(int source_kind, int ks) { return pick_source<RCH_PREC_FP16>(source_kind, ks); }
 
-FastFn pick_fast_fp16(int ks, bool rope, int out_dtype, bool head_pairs, int* chosen) {
-    return pick_fast<RCH_PREC_FP16>(ks, rope, out_dtype, head_pairs, chosen);
+FastFn pick_fast_fp16(int ks, bool rope, int out_dtype, int shape, int* chosen) {
+    return pick_fast<RCH_PREC_FP16>(ks, rope, out_dtype, shape, chosen);
 }
 
 SliceFn pick_slice_fp16(int ks, bool rope, int out_dtype, int* chosen, int* max_blocks) {

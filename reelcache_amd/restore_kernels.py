@@ -78,7 +78,8 @@ _MATRIX_CORE_PRECISIONS = ("fp32", "fp16", "fp16x2", "bf16")
 TILE_TOKENS = 128  # tokens per workgroup tile (4 waves x 32)
 SLICE_TOKENS = 32  # tokens per tile of the channel-slice kernel (one wave's MFMA columns)
 _DEFAULT_CONFIG = {"TILE_TOKENS": TILE_TOKENS, "BLOCK_N": 32, "waves": 4, "workgroups_per_cu": None,
-                   "store_cost": 4.0, "fast_variant": True, "slice_variant": False, "head_pairs": True}
+                   "store_cost": 4.0, "fast_variant": True, "slice_variant": False, "head_pairs": True,
+                   "split_rank": True}
 # Triton tile keys the reference accepts in ``config``; they have no meaning for the HIP
 # kernels and are accepted (and ignored) so that caller configurations keep working.
 _REFERENCE_TILE_KEYS = {"BLOCK_M", "BLOCK_K", "num_warps", "num_stages", "N_GROUP", "PIC_T", "UNPACK_BLOCK_K",
@@ -1330,6 +1331,7 @@ _FAST_LIMIT = 2 ** 31
 # larger ranks run the general kernel.
 _FAST_MAX_KSTEPS = {"fp16x2": 12, "fp16": 16, "bf16": 16, "fp32": 0}
 _PAIRS_MAX_KSTEPS = 12
+_SPLIT_MAX_KSTEPS = 32  # rank halves (RCH_GF_SPLIT_RANK): up to 512 ranks
 
 
 def _fast_flags(row, job, precision):
@@ -1370,8 +1372,8 @@ class _CallPlan:
         self.config = config
         self.keepalive = keepalive
         self.grids = []
-        self.variants = []  # per restore launch: "pairs" / "fast" (straight-line kernel, two or one
-        #                     heads per step), "sliced" (channel-slice kernel) or "general"
+        self.variants = []  # per restore launch: "pairs" / "fast" / "split" (straight-line kernel: two
+        #                     heads per step, one, or rank halves), "sliced" (channel-slice kernel) or "general"
 
     # -- per-job descriptor fields ------------------------------------------------------------
     # Rows are plain lists indexed by the rch_job field columns (``_JOB_INDEX``); one int64
@@ -1572,9 +1574,15 @@ class _CallPlan:
                 launches_planned.append(("dense", tile_offset, len(tiles), channels, head_dim, out_dtype))
                 continue
             if group_flags & _lib.GF_FAST and max_ksteps > _FAST_MAX_KSTEPS[precision]:
-                group_flags = 0  # no straight-line variant holds this many rank steps in registers
-            if (allow_pairs and group_flags & _lib.GF_FAST and (channels // head_dim) % 2 == 0
-                    and max_ksteps <= _PAIRS_MAX_KSTEPS):
+                # Beyond one wave's registers: rank halves in 8-wave workgroups (uint8 rows, up to
+                # 32 rank steps), else the general kernel.
+                allow_split = bool(_config_value(self.config, "split_rank"))
+                if allow_split and kind == _lib.SRC_U8 and max_ksteps <= _SPLIT_MAX_KSTEPS:
+                    group_flags = (group_flags & ~_lib.GF_HEAD_PAIRS) | _lib.GF_SPLIT_RANK
+                else:
+                    group_flags = 0
+            if (allow_pairs and group_flags & _lib.GF_FAST and not group_flags & _lib.GF_SPLIT_RANK
+                    and (channels // head_dim) % 2 == 0 and max_ksteps <= _PAIRS_MAX_KSTEPS):
                 group_flags |= _lib.GF_HEAD_PAIRS  # a work unit: one dim block of two heads
             blocks_per_tile = (channels + 31) // 32 // (2 if group_flags & _lib.GF_HEAD_PAIRS else 1)
             steps = np.array([job_steps[i] for i in tiles[:, 0].tolist()], dtype=np.float64)
@@ -1586,7 +1594,8 @@ class _CallPlan:
                                      kind, out_dtype, max_ksteps, group_flags))
             self.grids.append(grid)
             self.variants.append("general" if not group_flags & _lib.GF_FAST
-                                 else ("pairs" if group_flags & _lib.GF_HEAD_PAIRS else "fast"))
+                                 else ("pairs" if group_flags & _lib.GF_HEAD_PAIRS
+                                       else ("split" if group_flags & _lib.GF_SPLIT_RANK else "fast")))
         bound_tiles = _tiles(bound_jobs, jobs) if bound_jobs else None
         bound_tile_offset = arena.add(bound_tiles) if bound_jobs else None
         pack_desc = np.zeros(n_packs, dtype=_lib.PACK_DTYPE)
@@ -1671,7 +1680,8 @@ def _rank_class(precision, job):
     if job.rank is None:
         return 0
     steps = (job.rank + 15) // 16
-    classes = (4, 8) if precision == "fp32" else ((2, 4, 8, 12) if precision == "fp16x2" else (2, 4, 8, 12, 16))
+    # The 16-bit modes add the rank-halves variants' classes (24, 32; fp16x2 also 16).
+    classes = (4, 8) if precision == "fp32" else (2, 4, 8, 12, 16, 24, 32)
     for size in classes:
         if steps <= size:
             return size
@@ -1926,8 +1936,9 @@ class WarmupShape:
                 "native_rope_dtype": None if self.native_rope_dtype is None else str(self.native_rope_dtype)}
 
 
-# Register-resident rank steps of the compiled variants (their code objects load on first launch).
-_VARIANT_STEPS = (2, 4, 8, 12, 16, 17)
+# Register-resident rank steps of the compiled variants (their code objects load on first launch):
+# the one-wave classes, the rank-halves classes and the chunked general kernel beyond them.
+_VARIANT_STEPS = (2, 4, 8, 12, 16, 24, 32, 33)
 
 
 def _warmup_ranks(ranks):

@@ -8,7 +8,8 @@ Three chunks per target keep the oracle affordable; the checks are
     are untouched;
   * sampled token rows of every job against the oracle's elementwise error bound
     (reelcache/restore_kernels.py:1208-1227).
-Ranks above 192 (fp16x2) have no straight-line variant, so these groups run the general kernel.
+Ranks above 192 (fp16x2) run the rank-halves variant of the straight-line kernel (8-wave
+workgroups, two halves of the rank steps reduced through LDS).
 """
 
 import numpy as np
@@ -42,7 +43,7 @@ def test_longcat_shape_restore(device):
                                    view=view, basis=basis, out_dtype="bfloat16", device=device))
     handle = rk.reconstruct([case.job for case in cases])
     handle.release()
-    assert handle.stats["variants"] and set(handle.stats["variants"]) == {"general"}, handle.stats["variants"]
+    assert handle.stats["variants"] and set(handle.stats["variants"]) == {"split"}, handle.stats["variants"]
     for cache in caches:
         tokens_major = cache[0].transpose(0, 1)  # [T, H, D]
         assert not bool((tokens_major[7:7 + history] == FILL).any()), "a slot element was not written"

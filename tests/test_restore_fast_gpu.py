@@ -119,3 +119,41 @@ def test_unaligned_jobs_use_the_general_kernel(device):
     handle.release()
     assert handle.stats["variants"] == ["general"]  # rows of 33 bytes are not 16-byte aligned
     _check_bound(case, "fp16x2")
+
+
+# (heads, head_dim, rank, rope, grid): ranks beyond one wave's registers (rank halves)
+SPLIT_SHAPES = [
+    (4, 128, 200, "separable", (2, 9, 13)),   # fp16x2: 13 steps -> halves of 8
+    (6, 64, 300, "none", (1, 16, 9)),         # 19 steps -> halves of 12, one partial tile
+    (5, 128, 500, "dense", (3, 7, 11)),       # 32 steps -> halves of 16, ragged last tile
+]
+
+
+@pytest.mark.parametrize("precision", ["fp16x2", "fp16", "bf16"])
+@pytest.mark.parametrize("out_dtype", ["bfloat16", "float32"])
+def test_rank_halves_match_general_and_oracle(device, precision, out_dtype):
+    """Ranks beyond one wave's registers run the rank-halves kernel (8-wave workgroups, the high
+    half's fp32 partial sums added through LDS): within the oracle's bound like the general
+    kernel, and equal to it except where the different fp32 summation order moves a final
+    rounding (a small fraction of elements)."""
+    limit = 12 if precision == "fp16x2" else 16
+    for index, (heads, head_dim, rank, rope, grid) in enumerate(SPLIT_SHAPES):
+        seed = zlib.crc32(f"split/{precision}/{out_dtype}/{index}".encode())
+        cases = []
+        for _ in range(2):
+            rng = np.random.default_rng(seed)
+            cases.append(make_case(rng, grid=grid, heads=heads, head_dim=head_dim, rank=rank, source="uint8",
+                                   rope=rope, out_dtype=out_dtype, device=device, token_offset=3,
+                                   code_pitch=-(-rank // 16) * 16))  # 16-byte aligned code rows
+        handle = rk.reconstruct([cases[0].job], precision=precision)
+        handle.release()
+        steps = (rank + 15) // 16
+        want = ["split"] if steps > limit else ["fast" if heads % 2 or steps > 12 else "pairs"]
+        assert handle.stats["variants"] == want, (rank, handle.stats["variants"])
+        assert _run(cases[1], precision, "general") == ["general"]
+        _check_bound(cases[0], precision)
+        _check_bound(cases[1], precision)
+        ours, general = written(cases[0]), written(cases[1])
+        if out_dtype != "float32":  # fp32 outputs keep the summation order's last bits
+            differ = float((ours != general).mean())
+            assert differ <= 0.02, f"rank {rank}: {differ:.4f} of elements differ from the general kernel"
