@@ -15,7 +15,9 @@ Printed JSON line (one): ``value`` = restored KV bytes written per second
 (GB/s, whole job), ``ms_per_step``, per-layer latency, the ``roofline`` of the
 fused restore kernel (algorithmic bytes per launch / its average duration,
 measured with HIP events on the launch stream) and a ``cpu_baseline`` (the
-oracle's CPU restatement on a bounded sample, timed on this host).
+oracle's CPU restatement on a bounded sample, timed on this host).  Beside the headline:
+``longcat`` (per-layer restore time at the BASELINE configs[4] shape, MFMA roofline, alone and
+beside a concurrent GEMM) and ``fit`` (BASELINE configs[2] chunks per second).
 """
 
 from __future__ import annotations
@@ -319,6 +321,85 @@ def fit_leg(device, steps, warmup, cpu_seconds):
     return result
 
 
+# ---------------------------------------------------------------------------------------------
+# LongCat leg: layer restores at the LongCat-Video shape, MFMA-bound.
+# ---------------------------------------------------------------------------------------------
+
+LC_CHUNKS, LC_HEADS, LC_MAX_RANK = 16, 32, 512
+
+
+def longcat_leg(device, layers, reps):
+    """Per-layer restore time at the LongCat shape: 16 chunks x 4680 tokens of K and V, 32 heads x
+    128 in the [1, H, T, D] bf16 cache layout, per-chunk ranks U{256..512} on the 32-grid of one
+    512-row orthonormal bf16 basis per layer and target, no RoPE (LongCat stores pre-RoPE K).
+    Timed with HIP events on the launch stream (pack -> last restore), alone and while a
+    4096 x 4096 bf16 GEMM runs on a second stream (the next chunk's forward)."""
+    from reelcache_amd import restore_kernels as rk
+
+    rng = np.random.default_rng(5)
+    generator = torch.Generator(device=device).manual_seed(5)
+    channels = LC_HEADS * HEAD_DIM
+    history = LC_CHUNKS * TOKENS
+    work = []
+    flops = 0
+    for _ in range(layers):
+        jobs = []
+        for _target in range(2):
+            cache = torch.empty((1, LC_HEADS, history, HEAD_DIM), dtype=torch.bfloat16, device=device)
+            gauss = torch.randn(channels, LC_MAX_RANK, device=device, generator=generator, dtype=torch.float32)
+            basis = torch.linalg.qr(gauss).Q.T.contiguous().to(torch.bfloat16)
+            for chunk in range(LC_CHUNKS):
+                rank = int(rng.integers(8, 17)) * 32
+                codes = torch.randint(0, 256, (TOKENS, rank), dtype=torch.uint8, device=device, generator=generator)
+                scale, offset = covering_affine(rank, rng)
+                jobs.append(rk.ReconstructionJob(rk.CoefficientSource(codes, scale, offset),
+                                                 rk.NativeView(cache, layout="BHTD", token_offset=chunk * TOKENS),
+                                                 GRID, basis, rank, None))
+                flops += 2 * TOKENS * channels * rank
+        work.append(jobs)
+    flops //= layers
+    stream = torch.cuda.Stream(device)
+    side = torch.cuda.Stream(device)
+    a = torch.randn(4096, 4096, device=device, dtype=torch.bfloat16, generator=generator)
+    b = torch.randn(4096, 4096, device=device, dtype=torch.bfloat16, generator=generator)
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            a @ b
+    for jobs in work:
+        rk.reconstruct(jobs, stream=stream).release()
+    torch.cuda.synchronize(device)
+    results = {}
+    variants = []
+    for mode in ("alone", "with_gemm"):
+        times = []
+        for _ in range(reps):
+            for jobs in work:
+                if mode == "with_gemm":
+                    side.wait_stream(stream)
+                    with torch.cuda.stream(side):
+                        a @ b
+                stage = []
+                handle = rk.reconstruct(jobs, stream=stream, stage_events=stage)
+                handle.release()
+                variants = handle.stats["variants"]
+                stream.synchronize()
+                side.synchronize()
+                events = dict(stage)
+                times.append(events["pack"].elapsed_time(events["fused"]) * 1e3)
+        results[mode] = float(np.median(times))
+    del work
+    torch.cuda.empty_cache()
+    alone = results["alone"]
+    return {"workload": "BASELINE configs[4] shape: 16 chunks x 4680 tokens x {K,V}, 32x128 BHTD bf16, ranks "
+                        "U{256..512} on the 32-grid (one 512-row bf16 basis per layer and target), no RoPE, fp16x2",
+            "layers": layers, "kernel_us_per_layer": round(alone, 1),
+            "kernel_us_per_layer_with_gemm": round(results["with_gemm"], 1),
+            "gflop_per_layer": round(flops / 1e9, 1), "variants": variants,
+            "roofline": {"bound": "mfma", "achieved": round(flops / (alone / 1e6) / 1e12, 1), "peak": 2500.0,
+                         "unit": "TFLOP/s", "frac": round(flops / (alone / 1e6) / 1e12 / 2500.0, 4),
+                         "mfma_work_tflops": round(2 * flops / (alone / 1e6) / 1e12, 1)}}
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
@@ -328,6 +409,8 @@ def main():
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--fit-steps", type=int, default=2, help="timed fit chunks (0 skips the fit leg)")
     parser.add_argument("--fit-warmup", type=int, default=1)
+    parser.add_argument("--longcat-layers", type=int, default=2,
+                        help="LongCat-shape layers timed beside the headline (0 skips the leg)")
     parser.add_argument("--copy-probe", action="store_true",
                         help="after the timed region, run 3 plain device copies of 256 MiB (the calibration "
                              "dispatches for rocprofv3 FETCH_SIZE / WRITE_SIZE passes)")
@@ -429,9 +512,11 @@ def main():
         torch.cuda.synchronize(device)
         del source, target
     del graph, captured
+    del layers, handles
+    torch.cuda.empty_cache()
+    if args.longcat_layers > 0:
+        result["longcat"] = longcat_leg(device, args.longcat_layers, 3)
     if args.fit_steps > 0:
-        del layers, handles
-        torch.cuda.empty_cache()
         result.update(fit_leg(device, args.fit_steps, args.fit_warmup,
                               0.0 if args.no_cpu_baseline else args.cpu_seconds))
     if not args.no_cpu_baseline:
