@@ -74,6 +74,7 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
     __shared__ __attribute__((aligned(16))) uint8_t codes[kCodesBytes];
     __shared__ __attribute__((aligned(16))) float affine[2 * kRanks];
     __shared__ int block_exp[kFastMaxBlocks];  // basis block exponents of the current tile's job
+    __shared__ int64_t cell_offset[kRanks];    // pictures: byte offset of rank column k's cell in a picture
 
     const int range = xcd_unit(blockIdx.x, gridDim.x);
     const int first_unit = bounds[range];
@@ -242,7 +243,46 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
                     out[1] = u2{b[2], b[3]};
                 }
             }
-        } else {  // pictures: one thread per (token, half of the rank columns), 16 gathers in flight
+        } else if (J->pic_slots >= rank) {
+            // Pictures of one segment (channel_tiles.v1: rank column k in cell k of every frame's
+            // picture).  The cells' offsets within a picture are tabulated in LDS; then thread
+            // (token, p) gathers the columns of blocks [32 b + 16 p, + 16) of its token: a wave's
+            // lanes are 64 consecutive tokens, so each byte load of one column reads contiguous
+            // runs of a cell row, and a block's 16 loads are in flight together.
+            for (int k = tid; k < kRanks; k += kThreadsT) {
+                const int planes = static_cast<int>(J->pic_planes), cols = static_cast<int>(J->pic_grid_cols);
+                const int plane = k % planes, index = k / planes;
+                const int cell_row = index / cols, cell_col = index - cell_row * cols;
+                cell_offset[k] = plane * J->pic_plane_stride + static_cast<int64_t>(cell_row) * J->grid_h * J->pic_row_stride +
+                                 static_cast<int64_t>(cell_col) * J->grid_w;
+            }
+            __syncthreads();
+            const int token = tid & (kTileTokens - 1), p = tid / kTileTokens;  // p is wave-uniform
+            constexpr int kParts = kThreadsT / kTileTokens;
+            const int64_t tt = t0 + token;
+            const bool live = tt < tokens;
+            const Coords c = coords(J, live ? static_cast<int>(tt) : 0);
+            const RCH_GLOBAL uint8_t* base = gin<uint8_t>(J->src_ptr);
+            const int64_t lane = gin<int64_t>(J->pic_table_ptr)[c.f] + c.y * J->pic_row_stride + c.x;
+            uint8_t* row = codes + token * kPitch;
+            for (int b = p; 16 * b < kRanks; b += kParts) {
+                uint32_t got[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int k = 16 * b + i;
+                    const bool take = live & (k < rank);
+                    got[i] = base[take ? lane + cell_offset[k] : 0];  // byte 0 of the first picture is readable
+                    got[i] = take ? got[i] : 0u;
+                }
+                u4 word;
+#pragma unroll
+                for (int w = 0; w < 4; ++w)
+                    word[w] = got[4 * w] | (got[4 * w + 1] << 8) | (got[4 * w + 2] << 16) | (got[4 * w + 3] << 24);
+                u2* out = reinterpret_cast<u2*>(row + 16 * b);
+                out[0] = u2{word[0], word[1]};
+                out[1] = u2{word[2], word[3]};
+            }
+        } else {  // pictures of several segments: one thread per (token, half of the rank columns)
             const int token = tid >> 1, half = tid & 1;
             const int64_t tt = t0 + token;
             uint8_t* row = codes + token * kPitch;

@@ -16,6 +16,7 @@ import numpy as np
 import pytest
 import torch
 
+from oracle import quantize as oq
 from oracle import restore as orc
 from reelcache_amd import restore_kernels as rk
 
@@ -157,3 +158,21 @@ def test_rank_halves_match_general_and_oracle(device, precision, out_dtype):
         if out_dtype != "float32":  # fp32 outputs keep the summation order's last bits
             differ = float((ours != general).mean())
             assert differ <= 0.02, f"rank {rank}: {differ:.4f} of elements differ from the general kernel"
+
+
+@pytest.mark.parametrize("grid,rank,heads", [((2, 12, 14), 96, 4),     # one segment (the coalesced gather)
+                                             ((1, 2100, 100), 40, 2)])  # two segments (cells of 2100 x 100)
+def test_fast_picture_segments(device, grid, rank, heads):
+    """Picture sources in the straight-line kernel: layouts of one segment take the coalesced
+    gather (cell offsets tabulated per tile), others the per-token gather; both equal the
+    general kernel bit for bit and stay within the oracle's bound."""
+    assert oq.video_layout(*grid, rank, "yuv444p")["segments"] == (1 if rank == 96 else 2)
+    cases = []
+    for _ in range(2):
+        rng = np.random.default_rng(53)
+        cases.append(make_case(rng, grid=grid, heads=heads, head_dim=32, rank=rank, source="pictures", rope="none",
+                               out_dtype="bfloat16", device=device))
+    assert _run(cases[0], "fp16x2", "fast") == ["fast"]
+    assert _run(cases[1], "fp16x2", "general") == ["general"]
+    assert np.array_equal(written(cases[0]), written(cases[1]))
+    _check_bound(cases[0], "fp16x2")
