@@ -16,8 +16,9 @@ Printed JSON line (one): ``value`` = restored KV bytes written per second
 fused restore kernel (algorithmic bytes per launch / its average duration,
 measured with HIP events on the launch stream) and a ``cpu_baseline`` (the
 oracle's CPU restatement on a bounded sample, timed on this host).  Beside the headline:
-``longcat`` (per-layer restore time at the BASELINE configs[4] shape, MFMA roofline, alone and
-beside a concurrent GEMM) and ``fit`` (BASELINE configs[2] chunks per second).
+``pictures`` (the same layers restored from picture canvases), ``longcat`` (per-layer restore
+time at the BASELINE configs[4] shape, MFMA roofline, alone and beside a concurrent GEMM) and
+``fit`` (BASELINE configs[2] chunks per second).
 """
 
 from __future__ import annotations
@@ -400,6 +401,46 @@ def longcat_leg(device, layers, reps):
                          "mfma_work_tflops": round(2 * flops / (alone / 1e6) / 1e12, 1)}}
 
 
+def pictures_leg(layers, device, reps=3):
+    """The same CausVid layers restored from channel_tiles.v1 picture canvases (the decoded-video
+    production source; codes laid out by ``node_packets.mosaic_device``) instead of uint8 rows:
+    per-layer kernel time with HIP events on the launch stream (pack -> last restore)."""
+    from reelcache_amd import node_packets as npk
+    from reelcache_amd import restore_kernels as rk
+    from reelcache_amd.quantize import video_layout
+
+    work = []
+    for jobs in layers:
+        pictured = []
+        for job in jobs:
+            frames = job.grid[0]
+            video = video_layout(*job.grid, job.rank, "yuv444p")
+            canvases = npk.mosaic_device(job.source.values.contiguous(), video)
+            indices = [[segment * frames + frame for frame in range(frames)] for segment in range(video["segments"])]
+            source = rk.PictureSource.from_canvases(canvases, video, indices, (0, 0), job.source.scale, job.source.offset)
+            pictured.append(rk.ReconstructionJob(source, job.destination, job.grid, job.basis, job.rank, job.rope))
+        work.append(pictured)
+    stream = torch.cuda.Stream(device)
+    for jobs in work:
+        rk.reconstruct(jobs, stream=stream).release()
+    times, variants = [], []
+    for _ in range(reps):
+        for jobs in work:
+            stage = []
+            handle = rk.reconstruct(jobs, stream=stream, stage_events=stage)
+            handle.release()
+            variants = handle.stats["variants"]
+            stream.synchronize()
+            events = dict(stage)
+            times.append(events["pack"].elapsed_time(events["fused"]) * 1e3)
+    kernel_us = float(np.median(times))
+    _, algorithmic = layer_bytes()
+    return {"workload": "BASELINE configs[1] layers with codes in channel_tiles.v1 yuv444p canvases (one picture per "
+                        "frame), gathered in the restore kernel", "layers": len(layers),
+            "kernel_us_per_layer": round(kernel_us, 1), "variants": variants,
+            "achieved_gbs": round(algorithmic / (kernel_us / 1e6) / 1e9, 1)}
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
@@ -512,6 +553,7 @@ def main():
         torch.cuda.synchronize(device)
         del source, target
     del graph, captured
+    result["pictures"] = pictures_leg(layers[:4], device)
     del layers, handles
     torch.cuda.empty_cache()
     if args.longcat_layers > 0:
