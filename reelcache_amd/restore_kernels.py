@@ -1189,6 +1189,20 @@ def _balanced_bounds(tile_costs, blocks_per_tile, grid):
     return np.maximum.accumulate(bounds).astype(np.int32)
 
 
+_MEMO: dict = {}
+
+
+def _memo(key, build):
+    """Tile tables and balanced ranges of recurring call shapes (pure functions of the key;
+    callers never modify the returned arrays).  A small table, cleared when it grows."""
+    value = _MEMO.get(key)
+    if value is None:
+        if len(_MEMO) >= 512:
+            _MEMO.clear()
+        value = _MEMO[key] = build()
+    return value
+
+
 def _config_value(config, name):
     return config.get(name, _DEFAULT_CONFIG[name])
 
@@ -1568,7 +1582,8 @@ class _CallPlan:
                     self.grids.append(slice_grid)
                     self.variants.append("sliced")
                     continue
-            tiles = _tiles(members, jobs)
+            shape = (tuple(members), tuple(jobs[i].tokens for i in members))
+            tiles = _memo(("tiles",) + shape, lambda: _tiles(members, jobs))
             tile_offset = arena.add(tiles)
             if kind == _lib.SRC_DENSE:
                 launches_planned.append(("dense", tile_offset, len(tiles), channels, head_dim, out_dtype))
@@ -1585,11 +1600,15 @@ class _CallPlan:
                     and (channels // head_dim) % 2 == 0 and max_ksteps <= _PAIRS_MAX_KSTEPS):
                 group_flags |= _lib.GF_HEAD_PAIRS  # a work unit: one dim block of two heads
             blocks_per_tile = (channels + 31) // 32 // (2 if group_flags & _lib.GF_HEAD_PAIRS else 1)
-            steps = np.array([job_steps[i] for i in tiles[:, 0].tolist()], dtype=np.float64)
             per_cu = self.config.get("workgroups_per_cu") or _occupancy(self.code, kind, max_ksteps, head_dim, out_dtype,
                                                                         group_flags)
             grid = int(max(1, min(len(tiles) * blocks_per_tile, compute_units * max(1, per_cu))))
-            bounds = _balanced_bounds(steps * passes + store_cost, blocks_per_tile, grid)
+
+            def balanced():
+                steps = np.array([job_steps[i] for i in tiles[:, 0].tolist()], dtype=np.float64)
+                return _balanced_bounds(steps * passes + store_cost, blocks_per_tile, grid)
+            bounds = _memo(("bounds",) + shape + (tuple(job_steps[i] for i in members), blocks_per_tile, grid, passes,
+                                                  store_cost), balanced)
             launches_planned.append(("restore", tile_offset, len(tiles), arena.add(bounds), grid, channels, head_dim,
                                      kind, out_dtype, max_ksteps, group_flags))
             self.grids.append(grid)
