@@ -1,7 +1,7 @@
 """GPU test of restores captured in a HIP graph.
 
 A call of K (RoPE) and V jobs is captured once per kernel variant (straight-line with two or one
-heads per step, channel-slice, general); the graph is replayed several times, with eager work and synchronizations between the
+heads per step or rank halves, channel-slice, general); the graph is replayed several times, with eager work and synchronizations between the
 replays and the destinations overwritten before each, and every replay must reproduce the eager
 result bit for bit.  Captured calls take their descriptor staging from memory reserved
 beforehand (``reserve_capture_staging``); the capture itself allocates no pinned memory and
@@ -20,7 +20,7 @@ from restore_cases import destination, make_case
 pytestmark = pytest.mark.gpu
 
 
-def _jobs(device):
+def _jobs(device, ranks=(96, 160)):
     rng = np.random.default_rng(70)
     table = rk.RopeTable.from_complex(torch.from_numpy(orc.wan_freqs(128, 64)))
     heads, head_dim, grid, tokens = 4, 128, (2, 9, 13), 234
@@ -28,18 +28,20 @@ def _jobs(device):
     cache_v = destination("BTHD", 2 * tokens, heads, head_dim, "bfloat16", device)
     jobs = []
     for chunk in range(2):
-        jobs.append(make_case(rng, grid=grid, heads=heads, head_dim=head_dim, rank=96, source="uint8",
+        jobs.append(make_case(rng, grid=grid, heads=heads, head_dim=head_dim, rank=ranks[0], source="uint8",
                               view=rk.NativeView(cache_k, token_offset=chunk * tokens), table=table,
                               rope_rows=(2 * chunk, 0, 0), out_dtype="bfloat16", device=device).job)
-        jobs.append(make_case(rng, grid=grid, heads=heads, head_dim=head_dim, rank=160, source="uint8",
+        jobs.append(make_case(rng, grid=grid, heads=heads, head_dim=head_dim, rank=ranks[1], source="uint8",
                               view=rk.NativeView(cache_v, token_offset=chunk * tokens), rope="none",
                               out_dtype="bfloat16", device=device).job)
     return jobs, (cache_k, cache_v)
 
 
-@pytest.mark.parametrize("config", [{}, {"head_pairs": False}, {"slice_variant": True}, {"fast_variant": False}])
-def test_captured_restore_replays_match_eager(device, config):
-    jobs, caches = _jobs(device)
+@pytest.mark.parametrize("config,ranks", [({}, (96, 160)), ({"head_pairs": False}, (96, 160)),
+                                          ({"slice_variant": True}, (96, 160)), ({"fast_variant": False}, (96, 160)),
+                                          ({}, (256, 448))])  # rank halves (8-wave workgroups)
+def test_captured_restore_replays_match_eager(device, config, ranks):
+    jobs, caches = _jobs(device, ranks)
     for cache in caches:
         cache.fill_(-3.0)
     rk.reconstruct(jobs, config=config).release()
