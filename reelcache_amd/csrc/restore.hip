@@ -33,16 +33,73 @@ __device__ __forceinline__ void basis_row8(const rch_pack& P, int dtype, bool ve
     for (int j = 0; j < 8; ++j) v[j] = c + j < P.channels ? load_value(P.src_ptr, base + j, dtype) : 0.0f;
 }
 
+// Max pass of a pack workgroup: max|Q| over rows row_lane + 32 u (all u with a row below the
+// rank) of the thread's 8 channels c .. c + 7, keeping row stage_row in stage.  Eight rows per
+// thread are in flight together (one pass up to rank 256); rows past the rank re-read the last
+// row (a duplicate does not change the maximum).  VEC: 16-byte aligned f16 / bf16 rows and a
+// channel count that is a multiple of 8, loaded as one 16-byte word per row with no branch
+// between the loads; else element loads.
+template <bool VEC>
+__device__ __forceinline__ float pack_max(const rch_pack& P, int dtype, int64_t c, int row_lane, int64_t stage_row,
+                                          float (&stage)[8]) {
+    constexpr int kRows = 8;
+    const bool in = c < P.channels;
+    const bool staged = stage_row < P.rank;
+    float m = 0.0f;
+    for (int64_t r0 = row_lane; r0 < P.rank; r0 += 32 * kRows) {
+        float v[kRows][8];
+        if constexpr (VEC) {
+            u4 raw[kRows];
+#pragma unroll
+            for (int u = 0; u < kRows; ++u) {
+                const int64_t r = min(r0 + 32 * u, P.rank - 1);
+                raw[u] = in ? *reinterpret_cast<const RCH_GLOBAL u4*>(P.src_ptr + 2 * (r * P.row_stride + c)) : u4{0u, 0u, 0u, 0u};
+            }
+            if (dtype == RCH_DT_F16) {
+#pragma unroll
+                for (int u = 0; u < kRows; ++u) {
+                    const h8 x = __builtin_bit_cast(h8, raw[u]);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) v[u][j] = static_cast<float>(x[j]);
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < kRows; ++u) {
+                    const bf8 x = __builtin_bit_cast(bf8, raw[u]);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) v[u][j] = static_cast<float>(x[j]);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < kRows; ++u) basis_row8(P, dtype, false, min(r0 + 32 * u, P.rank - 1), c, v[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < kRows; ++u) {
+            const bool mine = staged && r0 + 32 * u == stage_row;  // never a clamped re-read
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                m = fmaxf(m, fabsf(v[u][j]));
+                stage[j] = mine ? v[u][j] : stage[j];
+            }
+        }
+    }
+    return m;
+}
+
 // Packs rows Q[:rank] of each basis into MFMA A-operand fragments.  Workgroup (g, sp, p) owns
 // 32-channel blocks 2g, 2g + 1 and 16-row steps 2sp, 2sp + 1 of basis p.  Fragment (s, nb, lane)
 // holds Q[16 s + k_slot(h, j), 32 nb + block_channel(lane % 32)] for j = 0..7 (h = lane / 32).
 // Fp16 fragments of a non-fp16 basis are prescaled by 2**e per 32-channel block so that the
 // block's max|Q| lands in (2**13, 2**14] (exact powers of two; e is written to exps[nb] and
 // undone by the restore epilogue).  Every workgroup reduces the max of its blocks itself
-// (rows are re-read from L2), so one launch suffices.
+// (rows are re-read from L2), so one launch suffices; its own staged rows come from the same
+// loads, so the workgroup makes one round of global reads (up to rank 256).
 template <int PREC>
 __global__ void __launch_bounds__(256) basis_pack_kernel(const rch_pack* __restrict__ packs) {
-    const rch_pack& P = packs[blockIdx.z];
+    // The whole descriptor is read up front (one round of scalar loads): reading fields where they
+    // are used chains several dependent memory round trips.
+    const rch_pack P = packs[blockIdx.z];
     const int64_t nb0 = 2 * static_cast<int64_t>(blockIdx.x);
     const int64_t s0 = 2 * static_cast<int64_t>(blockIdx.y);
     if (nb0 >= P.nblocks || s0 >= P.ksteps) return;  // whole workgroup
@@ -56,21 +113,16 @@ __global__ void __launch_bounds__(256) basis_pack_kernel(const rch_pack* __restr
     __shared__ float tile[32][64 + 4];
     __shared__ float block_max[4][2];
     __shared__ int block_exp[2];
+    // Row 16 s0 + row_lane of the 64 channels (zero beyond the rank): the row this thread stages.
+    // 16 s0 = 32 blockIdx.y, so it is one of the rows row_lane + 32 u the max pass reads.
+    const int64_t stage_row = 16 * s0 + row_lane;
+    float stage[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) stage[j] = 0.0f;
     if (scaled) {
-        // Rows are read four at a time so their loads are in flight together; rows past the rank
-        // re-read the last row (a duplicate does not change the maximum).
-        constexpr int kRows = 4;
-        float m = 0.0f;
-        for (int64_t r0 = row_lane; r0 < P.rank; r0 += 32 * kRows) {
-            float v[kRows][8];
-#pragma unroll
-            for (int u = 0; u < kRows; ++u) basis_row8(P, dtype, vec, min(r0 + 32 * u, P.rank - 1), c_base + 8 * chunk, v[u]);
-#pragma unroll
-            for (int u = 0; u < kRows; ++u) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[u][j]));
-            }
-        }
+        const bool fast = vec && P.channels % 8 == 0;
+        float m = fast ? pack_max<true>(P, dtype, c_base + 8 * chunk, row_lane, stage_row, stage)
+                       : pack_max<false>(P, dtype, c_base + 8 * chunk, row_lane, stage_row, stage);
         // Block of this thread: chunk / 4.  Reduce over chunk bits 0-1 and the 8 row lanes of the wave.
         m = fmaxf(m, __shfl_xor(m, 1));
         m = fmaxf(m, __shfl_xor(m, 2));
@@ -79,30 +131,21 @@ __global__ void __launch_bounds__(256) basis_pack_kernel(const rch_pack* __restr
         m = fmaxf(m, __shfl_xor(m, 32));
         if ((tid & 63) == 0) block_max[tid >> 6][0] = m;
         if ((tid & 63) == 4) block_max[tid >> 6][1] = m;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) tile[row_lane][8 * chunk + j] = stage[j];
         __syncthreads();
         if (tid < 2) {
             const float b = fmaxf(fmaxf(block_max[0][tid], block_max[1][tid]), fmaxf(block_max[2][tid], block_max[3][tid]));
             block_exp[tid] = prescale_exponent(b);
         }
-    } else if (tid < 2) {
-        block_exp[tid] = 0;
+    } else {
+        if (stage_row < P.rank) basis_row8(P, dtype, vec, stage_row, c_base + 8 * chunk, stage);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) tile[row_lane][8 * chunk + j] = stage[j];
+        if (tid < 2) block_exp[tid] = 0;
     }
     __syncthreads();
     if (blockIdx.y == 0 && tid < 2 && nb0 + tid < P.nblocks) gout<int32_t>(P.exp_ptr)[nb0 + tid] = block_exp[tid];
-    // Stage rows 16 s0 .. 16 s0 + 31 (zero beyond the rank) of the 64 channels.
-    {
-        const int64_t r = 16 * s0 + row_lane;
-        float v[8];
-        if (r < P.rank) {
-            basis_row8(P, dtype, vec, r, c_base + 8 * chunk, v);
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = 0.0f;
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) tile[row_lane][8 * chunk + j] = v[j];
-    }
-    __syncthreads();
     // Thread -> fragment: step s0 + (tid / 128), block nb0 + (tid / 64) % 2, lane tid % 64.
     const int sl = tid >> 7, b = (tid >> 6) & 1, lane = tid & 63, h = lane >> 5;
     const int64_t s = s0 + sl, nb = nb0 + b;

@@ -28,9 +28,6 @@ struct Cursor {
     int tile, bp, head;
 };
 
-// Largest number of 32-channel blocks (channels / 32) the straight-line kernel accepts.
-constexpr int kFastMaxBlocks = 256;
-
 // Three resident workgroups per CU where the LDS footprint allows it (KS <= 12: at most
 // 51 KB each) and the step fits the 168-VGPR budget that implies without spills (the two
 // RoPE pair sets add 32 VGPRs, so RoPE variants get three only up to KS = 8).  Head-pair steps
@@ -73,7 +70,6 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
     __shared__ u4 lds[2][kBuffer];
     __shared__ __attribute__((aligned(16))) uint8_t codes[kCodesBytes];
     __shared__ __attribute__((aligned(16))) float affine[2 * kRanks];
-    __shared__ int block_exp[kFastMaxBlocks];  // basis block exponents of the current tile's job
     __shared__ int64_t cell_offset[kRanks];    // pictures: byte offset of rank column k's cell in a picture
 
     const int range = xcd_unit(blockIdx.x, gridDim.x);
@@ -142,6 +138,7 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
     uint32_t row_t = 0, row_h = 0, row_w = 0;  // byte offsets of this token's RoPE rows
     __amdgpu_buffer_rsrc_t dst = make_rsrc(0, 0), pairs = make_rsrc(0, 0);
     int coef_exp = 0, sec0 = 0, sec1 = 0, head_bytes = 0;
+    int bexp_base = 0;  // first scratch word of the tile's basis block exponents
     CoefFrag<PREC> cf[kKsWave];
 
     f4 rope_next[4], rope_now[4];  // RoPE pairs of the next / current dim block
@@ -183,8 +180,8 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
 
     // Tile entry: stage the tile's codes and affine in LDS, convert this wave's 32 tokens to
     // coefficient fragments.  All waves passed a barrier since they last read codes / affine
-    // (rank halves: the low half reads partial sums and block exponents after the step barrier,
-    // so the entry starts with a barrier of its own).
+    // (rank halves: the low half reads partial sums after the step barrier, so the entry starts
+    // with a barrier of its own).
     auto enter = [&](const rch_job* J, int t0, int first_bp) __attribute__((always_inline)) {
         if constexpr (SPLIT == 2) __syncthreads();
         const int64_t tokens = J->tokens;
@@ -214,7 +211,7 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
         head_bytes = static_cast<int>(J->dst_head_stride) * kEsize;
         const float pre = pow2f(coef_exp);  // folded into the staged affine
         const int rank = static_cast<int>(J->rank);
-        for (int i = tid; i < heads * head_blocks; i += kThreadsT) block_exp[i] = scratch[J->basis_exp_index + i];
+        bexp_base = static_cast<int>(J->basis_exp_index);
         if (SPLIT == 2 || J->pic_slots == 0) {  // uint8 rows, 16-byte aligned (rank halves: uint8 rows only)
             const int64_t rs = J->src_row_stride;
             constexpr int kGroups = kRanks / 16;
@@ -328,9 +325,9 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
     };
 
     // Epilogue of head x of a step: undo the exponents, RoPE, cast, store this lane's 16 channels.
-    auto epilogue = [&](const Cursor& c, int x, const f16v& acc, const f4 (&rope)[4]) __attribute__((always_inline)) {
+    auto epilogue = [&](const Cursor& c, int x, const f16v& acc, const f4 (&rope)[4], int block_e) __attribute__((always_inline)) {
         // Undo the coefficient prescale and the block's basis exponent (exact powers of two).
-        const int e = coef_exp + block_exp[(c.head + x) * head_blocks + c.bp];
+        const int e = coef_exp + block_e;
         float v[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) v[i] = __builtin_amdgcn_ldexpf(acc[i], -e);
@@ -382,6 +379,41 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
 #pragma unroll
             for (int x = 0; x < HP; ++x) window[x][j] = frags[x * kHeadFrags + j * kStepFrags];
         }
+        // Basis block exponents of the step's blocks: scalar loads (they do not queue behind the
+        // vector stores of earlier steps), issued before the products and used by the epilogue.
+        int block_e[HP];
+#pragma unroll
+        for (int x = 0; x < HP; ++x) block_e[x] = scratch[bexp_base + (c.head + x) * head_blocks + c.bp];
+        if constexpr (HP == 2) {
+            // Head 0's products, then head 1's products with head 0's epilogue placed between
+            // them: its VALU work and stores issue while the matrix pipe works on head 1.
+            f16v a0 = f16v{}, a1 = f16v{};
+            u4 next[kAhead + 1];
+#pragma unroll
+            for (int j = 0; j < kAhead; ++j) next[j] = frags[kHeadFrags + j * kStepFrags];
+#pragma unroll
+            for (int s = 0; s < kKsWave; ++s) {
+                if (s + kAhead < kKsWave) window[0][(s + kAhead) % (kAhead + 1)] = frags[(s + kAhead) * kStepFrags];
+                a0 = mfma_frag<PREC>(window[0][s % (kAhead + 1)], cf[s], a0);
+            }
+            __builtin_amdgcn_sched_barrier(0);  // keep the two product chains apart
+#pragma unroll
+            for (int s = 0; s < kKsWave; ++s) {
+                if (s + kAhead < kKsWave) next[(s + kAhead) % (kAhead + 1)] = frags[kHeadFrags + (s + kAhead) * kStepFrags];
+                a1 = mfma_frag<PREC>(next[s % (kAhead + 1)], cf[s], a1);
+            }
+            epilogue(c, 0, a0, rope, block_e[0]);
+            // Up to six VALU instructions of head 0's epilogue after each product of head 1.
+            constexpr int kProducts = PREC == RCH_PREC_FP16X2 ? 2 * kKsWave : kKsWave;
+#pragma unroll
+            for (int i = 0; i < kProducts; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
+            }
+            epilogue(c, 1, a1, rope, block_e[1]);
+            __syncthreads();
+            return;
+        }
         f16v acc[HP];
 #pragma unroll
         for (int x = 0; x < HP; ++x) acc[x] = f16v{};
@@ -395,7 +427,7 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
         }
         if constexpr (SPLIT == 1) {
 #pragma unroll
-            for (int x = 0; x < HP; ++x) epilogue(c, x, acc[x], rope);
+            for (int x = 0; x < HP; ++x) epilogue(c, x, acc[x], rope, block_e[x]);
             __syncthreads();
         } else {
             // Partial sums of the high half, lane-contiguous per accumulator element (one
@@ -410,7 +442,7 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
                 f16v sum = acc[0];
 #pragma unroll
                 for (int i = 0; i < 16; ++i) sum[i] += partial[i * 64];
-                epilogue(c, 0, sum, rope);
+                epilogue(c, 0, sum, rope, block_e[0]);
             }
         }
     };
