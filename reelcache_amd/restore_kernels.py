@@ -1682,6 +1682,8 @@ class _CallPlan:
                           base + bounds_offset, grid, channels, head_dim, kind, out_dtype, self.code, max_ksteps,
                           group_flags, scratch_base, hip_stream)
             launches += 1
+            if stage_events is not None:
+                stage_events.append((f"launch{launches}", _record(self.stream)))
         if stage_events is not None:
             stage_events.append(("fused", _record(self.stream)))
         return launches
@@ -1813,7 +1815,8 @@ def reconstruct(jobs, *, backend="auto", precision="auto", stream=None, wait_eve
     ``native_rope``: optional ``(pre_rope[N, H, D], job) -> post_rope`` used instead
     of the built-in rotation for jobs with RoPE.  ``config``: launch overrides
     (``workgroups_per_cu``, ``store_cost``).  ``stage_events``: optional list
-    receiving ``(stage, event)`` timing events ("start", "pack", "fused", "rope_store").
+    receiving ``(stage, event)`` timing events ("start", "pack", "launch<n>" after the n-th launch of the
+    call, "fused", "rope_store").
 
     Returns a :class:`RestoreHandle`; destinations are valid after its event.
     """
