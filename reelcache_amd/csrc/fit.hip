@@ -13,7 +13,7 @@
 //     exactly to FP64, products and sums on v_mfma_f64_16x16x4f64, P rounded once to fp32.
 //     The FP64 sum makes P the correctly rounded fp32 value of the exact dot product except
 //     within ~1e-13 relative of a rounding boundary, i.e. independent of summation order.
-//   * Energies: FP64 per element ((x - r) / s)^2, per-64-row partials, fixed-order totals.
+//   * Energies: FP64 sums of (x - r)^2 and x^2, divided by s^2 per 64-row partial, fixed-order totals.
 //   * Quantizer: FP64 (v - offset) / scale, round half to even, clamp to [0, 255].
 #include <type_traits>
 
@@ -347,6 +347,7 @@ __global__ void __launch_bounds__(kThreads) project_kernel(const rch_fit_matrix*
             const int k = r0 + 16 * b + i16;
             const uint32_t q_off =
                 (k < rank && c < channels) ? static_cast<uint32_t>((k * M->basis_stride + c) * 2) : kOutOfRange;
+            if (r0 + 16 * b >= rank) continue;  // uniform: a 16-rank block past the rank adds zeros
             double qv[8];
             load8<RCH_DT_F16>(qs, q_off, qv);
 #pragma unroll
@@ -449,12 +450,10 @@ __global__ void __launch_bounds__(kThreads) residual_kernel(const rch_fit_matrix
                 a = static_cast<double>(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xs, offset, 0, 0)));
             else
                 a = static_cast<double>(half_bits<DT>(__builtin_amdgcn_raw_buffer_load_b16(xs, offset, 0, 0)));
-            double e = a - acc[v];
+            const double e = a - acc[v];
             if (resid && c < channels && t_ok) resid[c] = static_cast<float>(e);
-            if (scaled) {
-                a = a / s;
-                e = e / s;
-            }
+            // The scale s is applied once per tile below: sum (a / s)^2 = (sum a^2) / s^2 up to
+            // the rounding of the FP64 sums (relative 1e-16), without two FP64 divisions per element.
             src += a * a;
             err += e * e;
         }
@@ -476,6 +475,10 @@ __global__ void __launch_bounds__(kThreads) residual_kernel(const rch_fit_matrix
         for (int w = 0; w < kThreads / 64; ++w) {
             a += part[0][w];
             b += part[1][w];
+        }
+        if (scaled) {
+            a = a / s / s;
+            b = b / s / s;
         }
         RCH_GLOBAL double* out = gout<double>(M->partial_ptr) + 2 * blockIdx.x;
         out[0] = a;
