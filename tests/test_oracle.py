@@ -2,7 +2,8 @@
 
 The oracle restates the reference's arithmetic; these tests check it against what fixes
 that arithmetic independently of the restatement:
-  * the reference's own known answers (tests/test_codecs.py:383-436, NormalizationTests);
+  * the reference's own known answers (tests/test_codecs.py:383-436, NormalizationTests), held
+    as data in tests/golden/quantizer_known_answers.json;
   * library routines that implement the same rounding (torch casts and float32 arithmetic);
   * closed forms and brute force (complex multiplication for RoPE, nearest code by search,
     explicit loops for the product and the picture cells);
@@ -10,7 +11,9 @@ that arithmetic independently of the restatement:
     emulated precision modes).
 """
 
+import json
 import math
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -25,43 +28,50 @@ from oracle import restore as orc
 # ---------------------------------------------------------------------------
 
 
+GOLDEN = json.loads((Path(__file__).resolve().parent / "golden" / "quantizer_known_answers.json").read_text())
+
+
 def test_leading_columns_known_answers():
-    coefficients = np.array([[-1000, -100, 1, 2], [1000, 100, 3, 4], [0, 0, 2, 3]], dtype=np.float32)
-    codes, affine, layout = oq.quantize(coefficients, "leading_columns", 0.5)
-    assert layout["protected_count"] == 2
-    assert layout["affine_shape"] == [2, 3]
-    assert float(affine[1, 0]) == 1
-    assert abs(float(affine[0, 0]) - 3 / 255) < 5e-8
+    case = GOLDEN["leading_columns"]
+    expect = case["expect"]
+    coefficients = np.array(case["coefficients"], dtype=np.float32)
+    codes, affine, layout = oq.quantize(coefficients, "leading_columns", case["fraction"])
+    assert layout["protected_count"] == expect["protected_count"]
+    assert layout["affine_shape"] == expect["affine_shape"]
+    assert float(affine[1, 0]) == expect["offset_first_protected"]
+    assert abs(float(affine[0, 0]) - expect["scale_first_protected"]) < expect["scale_tolerance"]
     reconstructed = oq.dequantize(codes, affine, layout)
-    assert np.abs(reconstructed[:, 2:] - coefficients[:, 2:]).max() < 0.01
+    assert np.abs(reconstructed[:, 2:] - coefficients[:, 2:]).max() < expect["max_abs_error_unprotected"]
     _, global_affine, _ = oq.quantize(coefficients, "global")
-    assert global_affine[0, 0] > affine[0, 0] * 100
+    assert global_affine[0, 0] > affine[0, 0] * expect["global_scale_ratio_min"]
 
 
 def test_protection_endpoints():
-    coefficients = np.arange(24, dtype=np.float32).reshape(6, 4)
+    case = GOLDEN["protection_endpoints"]
+    coefficients = np.arange(int(np.prod(case["coefficients_arange"])), dtype=np.float32).reshape(case["coefficients_arange"])
     q_all, a_all, l_all = oq.quantize(coefficients, "leading_columns", 1)
-    q_pc, a_pc, l_pc = oq.quantize(coefficients, "per_channel")
-    np.testing.assert_array_equal(a_all[:, 0], [0, 0])
+    q_pc, a_pc, l_pc = oq.quantize(coefficients, case["expect"]["fraction_1_equals"])
+    np.testing.assert_array_equal(a_all[:, 0], case["expect"]["fraction_1_first_affine"])
     np.testing.assert_array_equal(q_all, q_pc)
     np.testing.assert_array_equal(a_all[:, 1:], a_pc)
     q_none, a_none, _ = oq.quantize(coefficients, "leading_columns", 0)
-    q_global, a_global, _ = oq.quantize(coefficients, "global")
+    q_global, a_global, _ = oq.quantize(coefficients, case["expect"]["fraction_0_equals"])
     np.testing.assert_array_equal(q_none, q_global)
     np.testing.assert_array_equal(a_none, a_global)
     np.testing.assert_array_equal(oq.dequantize(q_all, a_all, l_all), oq.dequantize(q_pc, a_pc, l_pc))
 
 
 def test_constant_channels():
-    coefficients = np.tile(np.array([-10, 3, 6, 6], dtype=np.float32), (24, 1))
-    for normalization, fraction in (("per_channel", 1), ("leading_columns", 0.5)):
+    case = GOLDEN["constant_channels"]
+    coefficients = np.tile(np.array(case["row"], dtype=np.float32), (case["rows"], 1))
+    for normalization, fraction in case["cases"]:
         codes, affine, layout = oq.quantize(coefficients, normalization, fraction)
         assert np.all(affine[0] == 0)
         np.testing.assert_array_equal(oq.dequantize(np.full_like(codes, 255), affine, layout), coefficients)
-    uniform = np.full((24, 4), -7.0, dtype=np.float32)
+    uniform = np.full(case["uniform_shape"], case["uniform_value"], dtype=np.float32)
     codes, affine, layout = oq.quantize(uniform, "global")
     assert affine[0, 0] == 0
-    np.testing.assert_array_equal(oq.dequantize(codes + 13, affine, layout), uniform)
+    np.testing.assert_array_equal(oq.dequantize(codes + case["uniform_code_shift"], affine, layout), uniform)
 
 
 # ---------------------------------------------------------------------------
