@@ -124,13 +124,13 @@ def build_workload(device, seed=0):
     return layers
 
 
-def restore_step(layers, stream, events=None):
+def restore_step(layers, stream, events=None, precision="auto"):
     from reelcache_amd import restore_kernels as rk
 
     handles = []
     for index, jobs in enumerate(layers):
         stage = [] if events is not None else None
-        handles.append(rk.reconstruct(jobs, stream=stream, stage_events=stage))
+        handles.append(rk.reconstruct(jobs, stream=stream, stage_events=stage, precision=precision))
         if events is not None:
             events.append(stage)
     return handles
@@ -441,6 +441,43 @@ def pictures_leg(layers, device, reps=3):
             "achieved_gbs": round(algorithmic / (kernel_us / 1e6) / 1e9, 1)}
 
 
+def fp16_leg(layers, device, steps):
+    """The same step in the single-product fp16 precision mode (the reference's default is
+    fp16x2): coefficients prescaled to fp16, one 32x32x16 f16 product per 16 ranks.  Its parity
+    (every element within the oracle's fp16 error bound; rel-Frobenius at most 1e-3 against the
+    fp32 reconstruction, the BASELINE tolerance) is tested in tests/test_restore_gpu.py."""
+    from reelcache_amd import restore_kernels as rk
+
+    stream = torch.cuda.Stream(device)
+    with torch.cuda.stream(stream):
+        for handle in restore_step(layers, stream, precision="fp16"):
+            handle.release()
+    torch.cuda.synchronize(device)
+    rk.reserve_capture_staging(LAYERS * (64 << 10))
+    graph = torch.cuda.CUDAGraph()
+    capture_stream = torch.cuda.Stream(device)
+    capture_stream.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.graph(graph, stream=capture_stream):
+        captured = restore_step(layers, capture_stream, precision="fp16")
+    torch.cuda.synchronize(device)
+    graph.replay()
+    torch.cuda.synchronize(device)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    stop.record()
+    torch.cuda.synchronize(device)
+    ms = start.elapsed_time(stop) / steps
+    written, algorithmic = layer_bytes()
+    del graph, captured
+    return {"precision": "fp16", "ms_per_step": round(ms, 4),
+            "value": round(LAYERS * written / (ms / 1e3) / 1e9, 2),
+            "layer_us": round(ms / LAYERS * 1e3, 2),
+            "layer_achieved_gbs": round(algorithmic / (ms / LAYERS / 1e3) / 1e9, 1),
+            "what": "graph-replayed step in precision='fp16' (not the headline: the reference's default is fp16x2)"}
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
@@ -452,6 +489,8 @@ def main():
     parser.add_argument("--fit-warmup", type=int, default=1)
     parser.add_argument("--longcat-layers", type=int, default=2,
                         help="LongCat-shape layers timed beside the headline (0 skips the leg)")
+    parser.add_argument("--no-fp16-leg", dest="fp16_leg", action="store_false",
+                        help="skip the step timed in the single-product fp16 precision mode")
     parser.add_argument("--pictures-layers", type=int, default=4,
                         help="layers restored from picture canvases beside the headline (0 skips the leg)")
     parser.add_argument("--copy-probe", action="store_true",
@@ -561,6 +600,8 @@ def main():
         "fit_chunks_per_s": None,
     }
     print(f"restore: {ms_per_step:.2f} ms/step, kernel {kernel_avg * 1e3:.1f} us/layer", file=sys.stderr, flush=True)
+    if args.fp16_leg:
+        result["fp16"] = fp16_leg(layers, device, args.steps)
     if args.copy_probe:
         source = torch.empty(COPY_PROBE_BYTES, dtype=torch.uint8, device=device).fill_(7)
         target = torch.empty_like(source)
