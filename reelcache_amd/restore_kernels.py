@@ -240,40 +240,49 @@ def _upload_stream(device):
 
 
 class _KernelTables:
-    """Contiguous FP32 device copies of one table and the event that completes them."""
+    """FP32 device copies of one table -- ``cos``, ``sin`` and the interleaved ``pairs``
+    ``[rows, pairs, 2]`` the straight-line kernels read -- and the event that completes all three.
+
+    Every consumer stream waits on the event (``order_before``) until it has completed, so a
+    call on any stream that finds the cached entry cannot read a table before it is written."""
 
     __slots__ = ("cos", "event", "pairs", "sin", "staging", "stamp")
 
-    def __init__(self, cos, sin, stamp, event=None, staging=None):
-        self.cos, self.sin, self.stamp, self.event, self.staging = cos, sin, stamp, event, staging
-        self.pairs = None
+    def __init__(self, cos, sin, pairs, stamp, event=None, staging=None):
+        self.cos, self.sin, self.pairs, self.stamp, self.event, self.staging = cos, sin, pairs, stamp, event, staging
 
     @classmethod
     def make(cls, cos, sin, device, stream, stamp):
         on_device = device.type == "cuda"
-        if on_device and all(t.device == device and t.dtype == torch.float32 and t.is_contiguous() for t in (cos, sin)):
-            return cls(cos, sin, stamp)  # the caller's tensors, ordered like the other inputs
         with torch.inference_mode(False), torch.no_grad():
             if not on_device:
-                return cls(cos.to(device=device, dtype=torch.float32).contiguous(),
-                           sin.to(device=device, dtype=torch.float32).contiguous(), stamp)
+                cos32, sin32 = (t.to(device=device, dtype=torch.float32).contiguous() for t in (cos, sin))
+                return cls(cos32, sin32, torch.stack((cos32, sin32), dim=-1).contiguous(), stamp)
+            if torch.cuda.is_current_stream_capturing():
+                # Work enqueued now would only run when the graph replays, and eager calls
+                # before the first replay would read unwritten tables.
+                raise ConfigurationError("a RoPE table's device copy cannot be built during HIP-graph capture: "
+                                         "run one call with the table (or warmup) before capturing")
+            staging = None
             if cos.device.type == "cpu":
                 # Read the host tables now into private pinned memory; upload on a private stream.
                 staging = tuple(torch.empty(t.shape, dtype=torch.float32, pin_memory=True).copy_(t) for t in (cos, sin))
-                upload = _upload_stream(device)
-                with torch.cuda.stream(upload):
-                    copies = tuple(torch.empty(t.shape, dtype=torch.float32, device=device) for t in staging)
-                    for target, source in zip(copies, staging):
-                        target.copy_(source, non_blocking=True)
-                    event = torch.cuda.Event()
-                    event.record(upload)
-                return cls(*copies, stamp, event, staging)
-            stream = torch.cuda.current_stream(device) if stream is None else stream
-            with torch.cuda.stream(stream):
-                copies = tuple(t.to(device=device, dtype=torch.float32).contiguous() for t in (cos, sin))
+                work = _upload_stream(device)
+            else:
+                work = torch.cuda.current_stream(device) if stream is None else stream
+            with torch.cuda.stream(work):
+                if staging is not None:
+                    cos32, sin32 = (torch.empty(t.shape, dtype=torch.float32, device=device) for t in staging)
+                    cos32.copy_(staging[0], non_blocking=True)
+                    sin32.copy_(staging[1], non_blocking=True)
+                else:
+                    # A contiguous float32 device table is used in place; other dtypes / layouts
+                    # are converted after the work already enqueued on the caller's stream.
+                    cos32, sin32 = (t.to(device=device, dtype=torch.float32).contiguous() for t in (cos, sin))
+                pairs = torch.stack((cos32, sin32), dim=-1).contiguous()
                 event = torch.cuda.Event()
-                event.record(stream)
-            return cls(*copies, stamp, event)
+                event.record(work)
+            return cls(cos32, sin32, pairs, stamp, event, staging)
 
     def order_before(self, device, stream):
         """Make ``stream`` (default: current) wait for the copies; no-op once complete."""
@@ -429,19 +438,10 @@ class RopeTable:
         return entry.cos, entry.sin
 
     def kernel_pairs(self, device, stream=None):
-        """Interleaved float32 ``[rows, pairs, 2]`` (cos, sin) on ``device`` (built once per table
-        version, on ``stream``, from :meth:`kernel_tables`)."""
-        cos, sin = self.kernel_tables(device, stream)
-        entry = self._device_cache[cos.device]
-        if entry.pairs is None:
-            with torch.inference_mode(False), torch.no_grad():
-                if cos.device.type != "cuda":
-                    entry.pairs = torch.stack((cos, sin), dim=-1).contiguous()
-                else:
-                    stream = torch.cuda.current_stream(cos.device) if stream is None else stream
-                    with torch.cuda.stream(stream):
-                        entry.pairs = torch.stack((cos, sin), dim=-1).contiguous()
-        return entry.pairs
+        """Interleaved float32 ``[rows, pairs, 2]`` (cos, sin) on ``device``, valid for work enqueued
+        next on ``stream`` (built with :meth:`kernel_tables`' copies and ordered by the same event)."""
+        cos, _ = self.kernel_tables(device, stream)
+        return self._device_cache[cos.device].pairs
 
 
 @dataclass(frozen=True, eq=False)
@@ -1097,6 +1097,9 @@ def _coefficient_bounds(scales, offsets, starts):
 
 _STAGING_LOCK = threading.Lock()
 _STAGING: dict = {}  # "slab": [pinned uint8 tensor, bytes handed out]
+# Every slab that has handed out a region: captured graphs copy their descriptors from those
+# regions on every replay, so a slab is never released, also after a larger one replaces it.
+_RETIRED_SLABS: list = []
 
 
 def reserve_capture_staging(nbytes=1 << 20):
@@ -1112,7 +1115,13 @@ def reserve_capture_staging(nbytes=1 << 20):
     with _STAGING_LOCK:
         slab = _STAGING.get("slab")
         if slab is None or slab[0].numel() - slab[1] < nbytes:
-            _STAGING["slab"] = [torch.empty(max(int(nbytes), 1 << 20), dtype=torch.uint8, pin_memory=True), 0]
+            if slab is not None and slab[1] > 0:
+                _RETIRED_SLABS.append(slab[0])
+            _STAGING["slab"] = [_pinned_bytes(max(int(nbytes), 1 << 20)), 0]
+
+
+def _pinned_bytes(nbytes):
+    return torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
 
 
 def _capture_staging(nbytes):

@@ -7,9 +7,10 @@ and a fork v1b = v0 + 16..64 rows; ranks are ragged in [64, min(256, version row
 (one resident tip per chain, ancestors served as prefixes) and restored with one call per layer.
 
 Gather / indexing is checked bit for bit: the caches equal those of the same restore given
-explicit per-job copies of each version's prefix rows.  Values are checked against the oracle
-(rel-Frobenius <= 1e-3 against its bf16-cast fp32 reconstruction and the reference's elementwise
-bound on a token sample).
+explicit bases built from the test's own rows of each version (not from the cache's views).
+Values of one node per version (v0, v1, the v2 tip and the v1b fork) are checked against the
+oracle on every layer and target (rel-Frobenius <= 1e-3 against its bf16-cast fp32
+reconstruction and the reference's elementwise bound on a token sample).
 """
 
 import numpy as np
@@ -29,7 +30,9 @@ TOKENS, CHANNELS = 4680, 1536
 
 
 def _versions(rng, layers):
+    """The product's version store and the test's own rows of every version (root first)."""
     versions = ar.BasisVersions()
+    own = {}
     for layer in range(layers):
         for target in ("K", "V"):
             sizes = {"v0": 192, "v1": int(rng.integers(16, 65)), "v2": int(rng.integers(16, 65)),
@@ -38,13 +41,20 @@ def _versions(rng, layers):
             total = sum(sizes.values())
             q, _ = np.linalg.qr(rng.standard_normal((CHANNELS, total)))
             rows = torch.from_numpy(q.T.copy()).to(torch.float16)
-            start = 0
+            start, spans = 0, {}
             for name in ("v0", "v1", "v2", "v1b"):
                 ref = f"{layer}{target}:{name}"
                 parent = None if parents[name] is None else f"{layer}{target}:{parents[name]}"
                 versions.add(ref, parent, rows[start:start + sizes[name]])
+                spans[name] = (start, start + sizes[name])
                 start += sizes[name]
-    return versions
+            for name in ("v0", "v1", "v2", "v1b"):
+                chain, walk = [], name
+                while walk is not None:
+                    chain.append(spans[walk])
+                    walk = parents[walk]
+                own[f"{layer}{target}:{name}"] = torch.cat([rows[a:b] for a, b in reversed(chain)], 0)
+    return versions, own
 
 
 def _rank(rng, total):
@@ -56,7 +66,7 @@ def _rank(rng, total):
 def test_fork_history_gather_is_exact(device):
     rng = np.random.default_rng(60)
     layers = 2
-    versions = _versions(rng, layers)
+    versions, own = _versions(rng, layers)
     names = ["v0"] * 3 + ["v1"] * 3 + ["v2"] * 3 + ["v1b"] * 3
     nodes = []
     for index, name in enumerate(names):
@@ -86,10 +96,16 @@ def test_fork_history_gather_is_exact(device):
         handle.release()
         for token in pins:
             cache.release(token)
-        # The same jobs with explicit copies of each version prefix (no cache, no shared storage).
-        copies = [rk.ReconstructionJob(job.source, rk.NativeView(explicit[layer][job.label.split(":")[-1]],
-                                                                  token_offset=job.destination.token_offset),
-                                       job.grid, job.basis.clone(), job.rank, job.rope, job.label) for job in jobs]
+        # The same jobs with bases built from the test's own rows of each node's version.
+        matrix_of = {f"{node.node_id}:{layer}:{target}": node.matrices[(layer, target)]
+                     for node in nodes for target in "KV"}
+        copies = []
+        for job in jobs:
+            matrix = matrix_of[job.label]
+            basis = own[matrix.version][:matrix.rank].to(device)
+            copies.append(rk.ReconstructionJob(job.source, rk.NativeView(explicit[layer][job.label.split(":")[-1]],
+                                                                         token_offset=job.destination.token_offset),
+                                               job.grid, basis, job.rank, job.rope, job.label))
         rk.reconstruct(copies).release()
     torch.cuda.synchronize(device)
     stats = cache.stats()
@@ -98,18 +114,18 @@ def test_fork_history_gather_is_exact(device):
     for layer in range(layers):
         for target in "KV":
             assert torch.equal(gathered[layer][target], explicit[layer][target])
-    # Values of two nodes per target against the oracle.
-    for node in nodes[:: 5]:
+    # Values of one node per version (v0, v1, v2 tip, v1b fork) on every layer and target.
+    for node, layer in [(nodes[i], layer) for i in (0, 3, 6, 9) for layer in range(layers)]:
         for target in "KV":
-            matrix = node.matrices[(0, target)]
-            basis = versions.assemble(matrix.version)[:matrix.rank].numpy().astype(np.float64)
+            matrix = node.matrices[(layer, target)]
+            basis = own[matrix.version][:matrix.rank].numpy().astype(np.float64)
             coefficients = orc.dequantize(matrix.codes.cpu().numpy(), matrix.scale, matrix.offset)
             rope = None
             if target == "K":
                 rope = orc.rope_cos_sin(np.real(orc.wan_freqs(HEAD_DIM, 64)), np.imag(orc.wan_freqs(HEAD_DIM, 64)),
                                         orc.wan_sections(HEAD_DIM // 2), (node.token_start // (30 * 52), 0, 0), GRID)
             values = orc.reconstruct(coefficients, basis, HEADS, rope, compute=np.float32)
-            out = gathered[0][target][0, node.token_start:node.token_start + TOKENS].float().cpu().numpy()
+            out = gathered[layer][target][0, node.token_start:node.token_start + TOKENS].float().cpu().numpy()
             out = out.reshape(TOKENS, CHANNELS)
             # bf16 cache: compare with the oracle's one bf16 cast of the fp32 reconstruction.
             assert orc.relative_frobenius(out, orc.cast(values, "bfloat16")) <= 1e-3

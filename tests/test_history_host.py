@@ -113,3 +113,26 @@ def test_history_gather_restores_each_node_into_its_range():
     for (index, target), values in expected.items():
         written = caches[target][0, index * tokens:(index + 1) * tokens].reshape(tokens, channels).numpy()
         np.testing.assert_allclose(written, values.astype(np.float32), rtol=1e-6, atol=1e-6)
+
+
+def test_batch_uploads_cannot_evict_each_other():
+    """A budget that holds one tip but not two: the second upload of one acquire_many call must
+    not evict the first (held by the batch), so the call fails with CapacityError and leaves no
+    pin behind (reelcache/archive_restore.py:174-175)."""
+    rng = np.random.default_rng(5)
+    versions = ar.BasisVersions()
+    versions.add("a", None, _rows(rng, 8))
+    versions.add("b", None, _rows(rng, 6))  # a second root: no prefix sharing
+    one_tip = 8 * 16 * 2
+    cache = ar.DeviceBasisCache(versions, "cpu", one_tip + 16)
+    with pytest.raises(CapacityError):
+        cache.acquire_many([("a", 4), ("b", 3)])
+    stats = cache.stats()
+    assert stats["pinned"] == 0
+    # Each alone fits, and nothing leaked: both can be acquired and released in turn.
+    view, token = cache.acquire("b", 3)
+    assert tuple(view.shape) == (3, 16)
+    cache.release(token)
+    view, token = cache.acquire("a", 8)
+    cache.release(token)
+    assert cache.stats()["pinned"] == 0

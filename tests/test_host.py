@@ -279,3 +279,23 @@ def test_captured_calls_need_reserved_staging(monkeypatch):
     assert second.data_ptr() - slab.data_ptr() == 1024  # regions start 256-byte aligned
     with pytest.raises(ConfigurationError):
         rk._capture_staging(3000)  # 2048 + 3000 exceeds the 4096-byte slab
+
+
+def test_replaced_staging_slab_stays_alive(monkeypatch):
+    """A slab that handed out regions to captured calls is kept when a larger one replaces it
+    (captured graphs copy from those regions on every replay)."""
+    monkeypatch.setattr(rk, "_STAGING", {})
+    monkeypatch.setattr(rk, "_RETIRED_SLABS", [])
+    monkeypatch.setattr(rk, "_pinned_bytes", lambda n: torch.zeros(n, dtype=torch.uint8))
+    monkeypatch.setattr(rk.torch.cuda, "is_available", lambda: False)
+    rk.reserve_capture_staging(1 << 20)
+    first_slab = rk._STAGING["slab"][0]
+    region = rk._capture_staging(1 << 19)
+    rk.reserve_capture_staging(1 << 20)  # does not fit the rest of the first slab: a new slab
+    assert rk._STAGING["slab"][0] is not first_slab
+    assert any(kept is first_slab for kept in rk._RETIRED_SLABS)
+    assert region.data_ptr() == first_slab.data_ptr()
+    # An unused slab is simply replaced (nothing captured reads it).
+    unused = rk._STAGING["slab"][0]
+    rk.reserve_capture_staging(1 << 21)
+    assert not any(kept is unused for kept in rk._RETIRED_SLABS)
