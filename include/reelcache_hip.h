@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-#define RCH_ABI_VERSION 6
+#define RCH_ABI_VERSION 7
 
 /* Status codes (mapped to reelcache errors by the host). */
 #define RCH_OK 0
@@ -229,6 +229,32 @@ int rch_restore_sliced(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles
                        const rch_slice_entry* entries_dev, int n_entries, const int32_t* wg_entries_dev, int grid,
                        int channels, int head_dim, int out_dtype, int precision, int max_ksteps, int group_flags,
                        const int32_t* scratch_dev, void* stream);
+
+/*
+ * rch_basis_pack + rch_restore of one launch group that allocates nothing: the packed bases and
+ * their block exponents live in a static device array of the library (RCH_NOALLOC_SCRATCH_BYTES
+ * per device, held until the process ends) instead of memory the caller provides.  No
+ * counterpart in the reference: it is for callers that cannot allocate device memory (code under
+ * HIP-graph capture, tight serving loops, harnesses that forbid allocation).
+ *   packs_host  host array of the group's bases (at most RCH_NOALLOC_MAX_PACKS); dst_ptr and
+ *               exp_ptr are ignored: pack i's fragments go to byte
+ *               F_i = sum_{j<i} round_up(ksteps_j * nblocks_j * 64 * rch_fragment_bytes(precision), 256)
+ *               of the fragment region, its block exponents to word E_i = sum_{j<i} nblocks_j.
+ *   jobs_dev    as for rch_restore, except that a job of pack i carries pack_ptr = F_i (relative to
+ *               the fragment region) and basis_exp_index = E_i, and bound_index = -1 (no device
+ *               coefficient bounds: float sources in the fp16 modes need a host bound).
+ * The other arguments are those of rch_restore.  Sizes beyond the array return RCH_E_CONFIG with
+ * the sizes in the message.  Every call on a GPU shares its array, which keeps the last call's
+ * contents: calls that overlap on one GPU (on different streams, or from several threads without
+ * ordering) race; calls ordered on one stream do not.
+ */
+#define RCH_NOALLOC_SCRATCH_BYTES (32 << 20)
+#define RCH_NOALLOC_WORD_BYTES 65536
+#define RCH_NOALLOC_MAX_PACKS 8
+int rch_restore_noalloc(const rch_pack* packs_host, int n_packs, const rch_job* jobs_dev, int n_jobs,
+                        const int32_t* tiles_dev, int n_tiles, const int32_t* bounds_dev, int grid, int channels,
+                        int head_dim, int source_kind, int out_dtype, int precision, int max_ksteps, int group_flags,
+                        void* stream);
 
 /*
  * Dense rows -> RoPE -> cast -> native store (DenseSource jobs).

@@ -16,7 +16,7 @@ import numpy as np
 from .errors import ConfigurationError, UnsupportedError
 
 LIBRARY = Path(__file__).resolve().with_name("libreelcache_hip.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # Status codes (RCH_E_*).
 OK, E_CONFIG, E_UNSUPPORTED, E_LAUNCH = 0, 1, 2, 3
@@ -71,6 +71,7 @@ _SIGNATURES = {
     "rch_restore_slice_blocks": ([_i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i)], _i),
     "rch_restore_sliced": ([_p, _i, _p, _i, _p, _i, _p, _i, _i, _i, _i, _i, _i, _i, _p, _p], _i),
     "rch_rope_store": ([_p, _i, _p, _i, _i, _i, _i, _p], _i),
+    "rch_restore_noalloc": ([_p, _i, _p, _i, _p, _i, _p, _i, _i, _i, _i, _i, _i, _i, _i, _p], _i),
     "rch_fit_matrix_size": ([], _i),
     "rch_fit_absmax": ([_p, _i, _i, _i64, _i, _p], _i),
     "rch_fit_gram": ([_p, _i, _i, _i, _p], _i),

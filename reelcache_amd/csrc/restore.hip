@@ -3,6 +3,8 @@
 //
 // Reference: reelcache/restore_kernels.py (_bound_kernel :1588-1606, _rope_store_kernel
 // :1557-1585, _fused_group / _two_pass_group :2025-2121).
+#include <mutex>
+
 #include "restore_slice.h"
 
 namespace rch {
@@ -96,10 +98,7 @@ __device__ __forceinline__ float pack_max(const rch_pack& P, int dtype, int64_t 
 // (rows are re-read from L2), so one launch suffices; its own staged rows come from the same
 // loads, so the workgroup makes one round of global reads (up to rank 256).
 template <int PREC>
-__global__ void __launch_bounds__(256) basis_pack_kernel(const rch_pack* __restrict__ packs) {
-    // The whole descriptor is read up front (one round of scalar loads): reading fields where they
-    // are used chains several dependent memory round trips.
-    const rch_pack P = packs[blockIdx.z];
+__device__ __forceinline__ void basis_pack_body(const rch_pack P) {
     const int64_t nb0 = 2 * static_cast<int64_t>(blockIdx.x);
     const int64_t s0 = 2 * static_cast<int64_t>(blockIdx.y);
     if (nb0 >= P.nblocks || s0 >= P.ksteps) return;  // whole workgroup
@@ -171,6 +170,25 @@ __global__ void __launch_bounds__(256) basis_pack_kernel(const rch_pack* __restr
         for (int j = 0; j < 8; ++j) out[j] = static_cast<_Float16>(v[j] * pre);
         gout<h8>(P.dst_ptr)[q] = out;
     }
+}
+
+template <int PREC>
+__global__ void __launch_bounds__(256) basis_pack_kernel(const rch_pack* __restrict__ packs) {
+    // The whole descriptor is read up front (one round of scalar loads): reading fields where they
+    // are used chains several dependent memory round trips.
+    basis_pack_body<PREC>(packs[blockIdx.z]);
+}
+
+// Pack descriptors passed by value (the no-allocation entry point has no device memory of the
+// caller's to hold them).
+constexpr int kNoAllocMaxPacks = 8;
+struct PackArgs {
+    rch_pack pack[kNoAllocMaxPacks];
+};
+
+template <int PREC>
+__global__ void __launch_bounds__(256) basis_pack_args_kernel(const PackArgs args) {
+    basis_pack_body<PREC>(args.pack[blockIdx.z]);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -340,31 +358,49 @@ int rch_restore_occupancy(int precision, int source_kind, int max_ksteps, int he
     return RCH_OK;
 }
 
-int rch_restore(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev, int n_tiles, const int32_t* bounds_dev,
-                int grid, int channels, int head_dim, int source_kind, int out_dtype, int precision, int max_ksteps,
-                int group_flags, const int32_t* scratch_dev, void* stream) {
-    if (!jobs_dev || !tiles_dev || !bounds_dev || !scratch_dev || n_jobs <= 0 || n_tiles <= 0 || grid <= 0 || channels <= 0 ||
+static int check_restore_args(const char* what, const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev,
+                              int n_tiles, const int32_t* bounds_dev, int grid, int channels, int head_dim,
+                              int out_dtype, int max_ksteps, int group_flags) {
+    if (!jobs_dev || !tiles_dev || !bounds_dev || n_jobs <= 0 || n_tiles <= 0 || grid <= 0 || channels <= 0 ||
         head_dim <= 0 || head_dim % 2 || max_ksteps <= 0 ||
         static_cast<int64_t>(n_tiles) * ((channels + 31) / 32) > 0x7fffffff)
-        return fail(RCH_E_CONFIG, "rch_restore: invalid launch arguments");
-    if (!valid_out(out_dtype)) return fail(RCH_E_CONFIG, "rch_restore: output dtype must be f32, f16 or bf16");
+        return fail(RCH_E_CONFIG, "%s: invalid launch arguments", what);
+    if (!valid_out(out_dtype)) return fail(RCH_E_CONFIG, "%s: output dtype must be f32, f16 or bf16", what);
     if ((group_flags & RCH_GF_FAST) && channels % head_dim)
-        return fail(RCH_E_CONFIG, "rch_restore: RCH_GF_FAST needs channels == heads * head_dim");
+        return fail(RCH_E_CONFIG, "%s: RCH_GF_FAST needs channels == heads * head_dim", what);
     if ((group_flags & RCH_GF_HEAD_PAIRS) && (!(group_flags & RCH_GF_FAST) || (channels / head_dim) % 2))
-        return fail(RCH_E_CONFIG, "rch_restore: RCH_GF_HEAD_PAIRS needs RCH_GF_FAST and an even head count");
-    Launch launch;
-    const int status = pick_launch(precision, source_kind, max_ksteps, head_dim, out_dtype, group_flags, &launch);
-    if (status) return status;
+        return fail(RCH_E_CONFIG, "%s: RCH_GF_HEAD_PAIRS needs RCH_GF_FAST and an even head count", what);
+    return RCH_OK;
+}
+
+// Launches the kernel pick_launch chose for a group; pack_base is added to every rch_job.pack_ptr.
+static void launch_restore(const Launch& launch, const rch_job* jobs_dev, const int32_t* tiles_dev,
+                           const int32_t* bounds_dev, int grid, int channels, int head_dim, int out_dtype,
+                           int max_ksteps, const int32_t* scratch_dev, int64_t pack_base, hipStream_t s) {
     if (launch.fast) {
         hipLaunchKernelGGL(reinterpret_cast<FastFn>(const_cast<void*>(launch.fn)), dim3(static_cast<unsigned>(grid)),
-                           dim3(static_cast<unsigned>(launch.threads)), 0, as_stream(stream), jobs_dev, tiles_dev,
-                           bounds_dev, scratch_dev, channels / head_dim, head_dim);
+                           dim3(static_cast<unsigned>(launch.threads)), 0, s, jobs_dev, tiles_dev, bounds_dev,
+                           scratch_dev, pack_base, channels / head_dim, head_dim);
     } else {
         const int nk = launch.chunked ? (max_ksteps + launch.ks - 1) / launch.ks : 1;
         hipLaunchKernelGGL(reinterpret_cast<RestoreFn>(const_cast<void*>(launch.fn)), dim3(static_cast<unsigned>(grid)),
-                           dim3(kThreads), 0, as_stream(stream), jobs_dev, tiles_dev, bounds_dev, scratch_dev, nk,
-                           channels, head_dim, out_dtype);
+                           dim3(kThreads), 0, s, jobs_dev, tiles_dev, bounds_dev, scratch_dev, pack_base, nk, channels,
+                           head_dim, out_dtype);
     }
+}
+
+int rch_restore(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev, int n_tiles, const int32_t* bounds_dev,
+                int grid, int channels, int head_dim, int source_kind, int out_dtype, int precision, int max_ksteps,
+                int group_flags, const int32_t* scratch_dev, void* stream) {
+    if (!scratch_dev) return fail(RCH_E_CONFIG, "rch_restore: invalid launch arguments");
+    int status = check_restore_args("rch_restore", jobs_dev, n_jobs, tiles_dev, n_tiles, bounds_dev, grid, channels,
+                                    head_dim, out_dtype, max_ksteps, group_flags);
+    if (status) return status;
+    Launch launch;
+    status = pick_launch(precision, source_kind, max_ksteps, head_dim, out_dtype, group_flags, &launch);
+    if (status) return status;
+    launch_restore(launch, jobs_dev, tiles_dev, bounds_dev, grid, channels, head_dim, out_dtype, max_ksteps,
+                   scratch_dev, 0, as_stream(stream));
     return check_launch("rch_restore");
 }
 
@@ -426,6 +462,107 @@ int rch_rope_store(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev
     hipLaunchKernelGGL(rope_store_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, as_stream(stream),
                        jobs_dev, tiles_dev, c_tiles, channels, head_dim, out_dtype);
     return check_launch("rch_rope_store");
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------------------------
+// Restore without allocation (rch_restore_noalloc): the packed bases and their block exponents
+// live in this file's static device array instead of memory the caller allocates.
+// ---------------------------------------------------------------------------------------------
+
+// Bytes [0, RCH_NOALLOC_WORD_BYTES): int32 block exponents; the packed fragments follow.  Each GPU
+// the library runs on holds its own copy until the process ends.
+static __device__ __align__(256) uint8_t scratch[RCH_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_lock;
+void* scratch_ptr[kMaxDevices];  // device address of `scratch` per device, set on its first call
+
+// The current device's address of `scratch`.  In host code the array's name is only a stand-in:
+// every kernel argument and address computed here uses this pointer.
+int current_scratch(void** out) {
+    int device = -1;
+    hipError_t error = hipGetDevice(&device);
+    if (error != hipSuccess) return fail(RCH_E_LAUNCH, "rch_restore_noalloc: hipGetDevice: %s", hipGetErrorString(error));
+    if (device < 0 || device >= kMaxDevices) return fail(RCH_E_UNSUPPORTED, "rch_restore_noalloc: device %d", device);
+    std::lock_guard<std::mutex> hold(scratch_lock);
+    if (!scratch_ptr[device]) {
+        void* ptr = nullptr;
+        error = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (error != hipSuccess || !ptr)
+            return fail(RCH_E_LAUNCH, "rch_restore_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(error));
+        scratch_ptr[device] = ptr;
+    }
+    *out = scratch_ptr[device];
+    return RCH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int rch_restore_noalloc(const rch_pack* packs_host, int n_packs, const rch_job* jobs_dev, int n_jobs,
+                        const int32_t* tiles_dev, int n_tiles, const int32_t* bounds_dev, int grid, int channels,
+                        int head_dim, int source_kind, int out_dtype, int precision, int max_ksteps, int group_flags,
+                        void* stream) {
+    if (!packs_host || n_packs <= 0)
+        return fail(RCH_E_CONFIG, "rch_restore_noalloc: invalid pack descriptors");
+    if (n_packs > kNoAllocMaxPacks)
+        return fail(RCH_E_CONFIG, "rch_restore_noalloc: %d bases in one call, at most %d", n_packs, kNoAllocMaxPacks);
+    int status = check_restore_args("rch_restore_noalloc", jobs_dev, n_jobs, tiles_dev, n_tiles, bounds_dev, grid,
+                                    channels, head_dim, out_dtype, max_ksteps, group_flags);
+    if (status) return status;
+    if (precision != RCH_PREC_FP32 && precision != RCH_PREC_FP16 && precision != RCH_PREC_FP16X2 &&
+        precision != RCH_PREC_BF16)
+        return fail(RCH_E_UNSUPPORTED, "precision %d has no matrix-core path on gfx950", precision);
+    // The layout: pack i's exponents at word E_i = sum_{j<i} nblocks_j, its fragments at byte
+    // F_i = sum_{j<i} round_up(ksteps_j * nblocks_j * 64 * fragment bytes, 256) of the fragment region.
+    const int64_t fragment = rch_fragment_bytes(precision);
+    int64_t words = 0, bytes = 0, max_nblocks = 0, max_pack_steps = 0;
+    PackArgs args;
+    void* base = nullptr;
+    status = current_scratch(&base);
+    if (status) return status;
+    const int64_t word_base = reinterpret_cast<int64_t>(base);
+    const int64_t fragment_base = word_base + RCH_NOALLOC_WORD_BYTES;
+    for (int i = 0; i < n_packs; ++i) {
+        const rch_pack& P = packs_host[i];
+        if (P.rank <= 0 || P.channels <= 0 || P.ksteps != (P.rank + 15) / 16 || P.nblocks != 2 * ((P.channels + 63) / 64))
+            return fail(RCH_E_CONFIG, "rch_restore_noalloc: pack %d: ksteps / nblocks do not match its rank / channels", i);
+        args.pack[i] = P;
+        args.pack[i].exp_ptr = word_base + 4 * words;
+        args.pack[i].dst_ptr = fragment_base + bytes;
+        words += P.nblocks;
+        bytes += (P.ksteps * P.nblocks * 64 * fragment + 255) / 256 * 256;
+        max_nblocks = P.nblocks > max_nblocks ? P.nblocks : max_nblocks;
+        max_pack_steps = P.ksteps > max_pack_steps ? P.ksteps : max_pack_steps;
+    }
+    if (4 * words > RCH_NOALLOC_WORD_BYTES || bytes > RCH_NOALLOC_SCRATCH_BYTES - RCH_NOALLOC_WORD_BYTES)
+        return fail(RCH_E_CONFIG,
+                    "rch_restore_noalloc: the packed bases need %lld fragment bytes and %lld exponent words; the "
+                    "static scratch holds %d and %d",
+                    static_cast<long long>(bytes), static_cast<long long>(words),
+                    RCH_NOALLOC_SCRATCH_BYTES - RCH_NOALLOC_WORD_BYTES, RCH_NOALLOC_WORD_BYTES / 4);
+    Launch launch;
+    status = pick_launch(precision, source_kind, max_ksteps, head_dim, out_dtype, group_flags, &launch);
+    if (status) return status;
+    hipStream_t s = as_stream(stream);
+    const dim3 pack_grid(static_cast<unsigned>((max_nblocks + 1) / 2), static_cast<unsigned>((max_pack_steps + 1) / 2),
+                         static_cast<unsigned>(n_packs));
+    switch (precision) {
+        case RCH_PREC_FP32: hipLaunchKernelGGL(basis_pack_args_kernel<RCH_PREC_FP32>, pack_grid, dim3(256), 0, s, args); break;
+        case RCH_PREC_FP16: hipLaunchKernelGGL(basis_pack_args_kernel<RCH_PREC_FP16>, pack_grid, dim3(256), 0, s, args); break;
+        case RCH_PREC_FP16X2: hipLaunchKernelGGL(basis_pack_args_kernel<RCH_PREC_FP16X2>, pack_grid, dim3(256), 0, s, args); break;
+        default: hipLaunchKernelGGL(basis_pack_args_kernel<RCH_PREC_BF16>, pack_grid, dim3(256), 0, s, args); break;
+    }
+    status = check_launch("rch_restore_noalloc (basis pack)");
+    if (status) return status;
+    launch_restore(launch, jobs_dev, tiles_dev, bounds_dev, grid, channels, head_dim, out_dtype, max_ksteps,
+                   reinterpret_cast<const int32_t*>(base), fragment_base, s);
+    return check_launch("rch_restore_noalloc");
 }
 
 }  // extern "C"

@@ -47,8 +47,8 @@ constexpr int kFastOccupancy = HP == 2 ? 2 : (((KS <= 12 && !ROPE) || (KS <= 8 &
 template <int PREC, int KS, bool ROPE, int OUT, int HP, int SPLIT>
 __global__ void __launch_bounds__(kThreads * SPLIT, (SPLIT == 2 ? 1 : kFastOccupancy<KS, ROPE, HP>))
 restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict__ tiles,
-                    const int32_t* __restrict__ bounds, const int32_t* __restrict__ scratch, int heads,
-                    int head_dim) {
+                    const int32_t* __restrict__ bounds, const int32_t* __restrict__ scratch, int64_t pack_base,
+                    int heads, int head_dim) {
     static_assert(PREC != RCH_PREC_FP32, "the fp32 mode runs restore_kernel");
     static_assert(HP == 1 || HP == 2, "one or two heads per step");
     static_assert(SPLIT == 1 || (SPLIT == 2 && HP == 1 && KS % 8 == 0), "rank halves: one head per step");
@@ -113,7 +113,7 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
             const rch_job* J = jobs + tiles[2 * c.tile];
             const int ks = static_cast<int>((J->rank + 15) >> 4);
             const int nblocks = static_cast<int>(J->pack_nblocks);
-            pack = make_rsrc(J->pack_ptr, int64_t(ks) * nblocks * 1024);
+            pack = make_rsrc(pack_base + J->pack_ptr, int64_t(ks) * nblocks * 1024);
 #pragma unroll
             for (int i = 0; i < kPer; ++i) {
                 const int q = tid + i * kThreadsT;
@@ -499,7 +499,9 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
     }
 }
 
-typedef void (*FastFn)(const rch_job*, const int32_t*, const int32_t*, const int32_t*, int, int);
+// Kernel arguments: jobs, tiles, bounds, scratch words, pack_base (added to every rch_job.pack_ptr:
+// 0 for absolute fragment addresses), heads, head_dim.
+typedef void (*FastFn)(const rch_job*, const int32_t*, const int32_t*, const int32_t*, int64_t, int, int);
 
 // Work-unit shape of a straight-line launch.
 enum FastShape : int { kOneHead = 0, kHeadPairs = 1, kRankHalves = 2 };

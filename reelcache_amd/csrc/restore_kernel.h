@@ -334,8 +334,8 @@ __device__ __forceinline__ RopeRegs load_rope(const rch_job* J, int kind, int c0
 template <int PREC, int SRC, int KS, bool CHUNKED>
 __global__ void __launch_bounds__(kThreads, 2)
 restore_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict__ tiles,
-               const int32_t* __restrict__ bounds, const int32_t* __restrict__ scratch, int nk, int channels,
-               int head_dim, int out_dtype) {
+               const int32_t* __restrict__ bounds, const int32_t* __restrict__ scratch, int64_t pack_base, int nk,
+               int channels, int head_dim, int out_dtype) {
     constexpr int kFrag = PREC == RCH_PREC_FP32 ? 2 : 1;  // u4 per lane fragment
     constexpr int kStepFrags = 64 * kFrag;               // one 16-rank step of one 32-channel block
     constexpr int kBuffer = KS * kStepFrags;
@@ -375,7 +375,7 @@ restore_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict__ til
         locate(st, tile, block, kc);
         const rch_job* job = jobs + tiles[2 * tile];
         const int count = chunk_steps(job, kc) * kStepFrags;
-        const RCH_GLOBAL u4* pack = gin<u4>(job->pack_ptr);
+        const RCH_GLOBAL u4* pack = gin<u4>(pack_base + job->pack_ptr);
         const int64_t nblocks = job->pack_nblocks;
 #pragma unroll
         for (int i = 0; i < kPerThread; ++i) {
@@ -599,7 +599,9 @@ restore_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict__ til
 
 }  // namespace
 
-typedef void (*RestoreFn)(const rch_job*, const int32_t*, const int32_t*, const int32_t*, int, int, int, int);
+// Kernel arguments: jobs, tiles, bounds, scratch words, pack_base (added to every rch_job.pack_ptr),
+// rank chunks, channels, head_dim, output dtype.
+typedef void (*RestoreFn)(const rch_job*, const int32_t*, const int32_t*, const int32_t*, int64_t, int, int, int, int);
 
 // A compiled variant: kernel, its register-resident rank steps and whether it chunks the rank.
 struct RestoreVariant {

@@ -79,7 +79,7 @@ TILE_TOKENS = 128  # tokens per workgroup tile (4 waves x 32)
 SLICE_TOKENS = 32  # tokens per tile of the channel-slice kernel (one wave's MFMA columns)
 _DEFAULT_CONFIG = {"TILE_TOKENS": TILE_TOKENS, "BLOCK_N": 32, "waves": 4, "workgroups_per_cu": None,
                    "store_cost": 4.0, "fast_variant": True, "slice_variant": False, "head_pairs": True,
-                   "split_rank": True}
+                   "split_rank": True, "static_scratch": False}
 # Triton tile keys the reference accepts in ``config``; they have no meaning for the HIP
 # kernels and are accepted (and ignored) so that caller configurations keep working.
 _REFERENCE_TILE_KEYS = {"BLOCK_M", "BLOCK_K", "num_warps", "num_stages", "N_GROUP", "PIC_T", "UNPACK_BLOCK_K",
@@ -1566,7 +1566,13 @@ class _CallPlan:
         passes = 2 if precision == "fp16x2" else (4 if precision == "fp32" else 1)
         store_cost = float(_config_value(self.config, "store_cost"))
         launches_planned = []
-        allow_slice = allow_fast and bool(_config_value(self.config, "slice_variant"))
+        # static_scratch: each launch group packs its bases into the library's static device
+        # array (rch_restore_noalloc) instead of this call's buffer.
+        static = bool(_config_value(self.config, "static_scratch"))
+        if static and bound_jobs:
+            raise ConfigurationError("static_scratch restores hold no device coefficient bounds: float sources in "
+                                     "the fp16 modes need a host bound")
+        allow_slice = allow_fast and bool(_config_value(self.config, "slice_variant")) and not static
         allow_pairs = allow_fast and bool(_config_value(self.config, "head_pairs"))
         for key, members in groups.items():
             kind, group_flags = key[0], key[-1]
@@ -1618,8 +1624,20 @@ class _CallPlan:
                 return _balanced_bounds(steps * passes + store_cost, blocks_per_tile, grid)
             bounds = _memo(("bounds",) + shape + (tuple(job_steps[i] for i in members), blocks_per_tile, grid, passes,
                                                   store_cost), balanced)
+            group_packs = None
+            if static:
+                # The documented layout of rch_restore_noalloc: pack i of the group at fragment byte
+                # F_i and exponent word E_i (sums over the group's earlier packs).
+                group_packs = list(dict.fromkeys(pack_index[basis_key[i]] for i in members))
+                placed, fragment_at, word_at = {}, 0, 0
+                for pack in group_packs:
+                    placed[pack] = (fragment_at, word_at)
+                    fragment_at += (ksteps[pack] * nblocks[pack] * 64 * fragment + 255) // 256 * 256
+                    word_at += nblocks[pack]
+                for i in members:
+                    rows[i][_C_PACK_PTR], rows[i][_C_EXP_INDEX] = placed[pack_index[basis_key[i]]]
             launches_planned.append(("restore", tile_offset, len(tiles), arena.add(bounds), grid, channels, head_dim,
-                                     kind, out_dtype, max_ksteps, group_flags))
+                                     kind, out_dtype, max_ksteps, group_flags, group_packs))
             self.grids.append(grid)
             self.variants.append("general" if not group_flags & _lib.GF_FAST
                                  else ("pairs" if group_flags & _lib.GF_HEAD_PAIRS
@@ -1632,6 +1650,8 @@ class _CallPlan:
 
         # One device buffer per call: [host tables | packed bases | scratch words].
         arena_bytes = (arena.size + 255) // 256 * 256
+        if static:
+            pack_total = 0  # the packs live in the library's static array
         scratch_words = bound_first + len(jobs)
         buffer = torch.empty(arena_bytes + pack_total + 4 * scratch_words + 256, dtype=torch.uint8, device=self.device)
         base = buffer.data_ptr()
@@ -1651,8 +1671,9 @@ class _CallPlan:
             entry["exp_ptr"] = scratch_base + 4 * exp_first[index]
         for index, column, offset in arena_refs:
             rows[index][column] = base + offset
-        for index, pack in pack_refs:
-            rows[index][_C_PACK_PTR] = pack_base + pack_offsets[pack]
+        if not static:
+            for index, pack in pack_refs:
+                rows[index][_C_PACK_PTR] = pack_base + pack_offsets[pack]
         if n_packs:
             arena.put(packs_offset, pack_desc)
         arena.put(desc_offset, np.array(rows, dtype=np.int64))
@@ -1663,7 +1684,7 @@ class _CallPlan:
         launches = 0
         if stage_events is not None:
             stage_events.append(("start", _record(self.stream)))
-        if n_packs:
+        if n_packs and not static:
             _lib.call("rch_basis_pack", base + packs_offset, n_packs, int(max(nblocks)), int(max(ksteps)), self.code,
                       hip_stream)
             launches += 1
@@ -1686,10 +1707,16 @@ class _CallPlan:
                           self.code, max_ksteps, group_flags, scratch_base, hip_stream)
             else:
                 (_, tile_offset, n_tiles, bounds_offset, grid, channels, head_dim, kind, out_dtype, max_ksteps,
-                 group_flags) = plan
-                _lib.call("rch_restore", base + desc_offset, len(jobs), base + tile_offset, n_tiles,
-                          base + bounds_offset, grid, channels, head_dim, kind, out_dtype, self.code, max_ksteps,
-                          group_flags, scratch_base, hip_stream)
+                 group_flags, group_packs) = plan
+                if group_packs is None:
+                    _lib.call("rch_restore", base + desc_offset, len(jobs), base + tile_offset, n_tiles,
+                              base + bounds_offset, grid, channels, head_dim, kind, out_dtype, self.code, max_ksteps,
+                              group_flags, scratch_base, hip_stream)
+                else:
+                    host_packs = np.ascontiguousarray(pack_desc[group_packs])
+                    _lib.call("rch_restore_noalloc", host_packs.ctypes.data, len(group_packs), base + desc_offset,
+                              len(jobs), base + tile_offset, n_tiles, base + bounds_offset, grid, channels, head_dim,
+                              kind, out_dtype, self.code, max_ksteps, group_flags, hip_stream)
             launches += 1
             if stage_events is not None:
                 stage_events.append((f"launch{launches}", _record(self.stream)))
