@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-#define RCH_ABI_VERSION 7
+#define RCH_ABI_VERSION 8
 
 /* Status codes (mapped to reelcache errors by the host). */
 #define RCH_OK 0
@@ -71,6 +71,18 @@ extern "C" {
                                for max_ksteps <= 12 (RCH_E_CONFIG otherwise).  Straight-line
                                variants cover max_ksteps <= 12 (fp16x2) or 16 (fp16, bf16); larger
                                ranks run the general kernel whatever the flags. */
+#define RCH_GF_STREAM 16   /* with RCH_GF_FAST, fp16x2, uint8 code rows, head_dim 128, channels % 128 == 0,
+                              max_ksteps <= 16, no other shape flag: the basis-stationary stream kernel.
+                              Work units are (job, head, 32-token tile), job-major; tiles_dev holds
+                              int32 [n_members + 1][2]: (first unit, job index) of each job of the group,
+                              then (total units, 0); each job's pack_ptr points to its RCH_PACK_STREAM
+                              slabs.  Its arithmetic folds the affine into the basis (exact fp16 codes),
+                              so its output may differ from the other kernels' in the last bits. */
+#define RCH_GF_DENSE_ROPE 32 /* with RCH_GF_STREAM and RCH_GF_ROPE: every job's table is dense (one row per
+                               token).  Without it every job's table is separable and its section rows
+                               (frames * sec_t + grid_h * sec_h + grid_w * sec_w pairs) number at most
+                               RCH_STREAM_SECTION_PAIRS: the stream kernel stages them in LDS per job. */
+#define RCH_STREAM_SECTION_PAIRS 2048
 #define RCH_GF_SPLIT_RANK 8 /* with RCH_GF_FAST, uint8 code rows, not with RCH_GF_HEAD_PAIRS: the
                                straight-line kernel with 8-wave workgroups that split the rank
                                steps in two halves (max_ksteps up to 32); work units as without
@@ -122,13 +134,23 @@ typedef struct rch_pack {
     int64_t row_stride;      /* elements */
     int64_t rank;
     int64_t channels;
-    int64_t dst_ptr;         /* packed fragments: ksteps * nblocks * 64 * frag bytes */
-    int64_t ksteps;          /* ceil(rank / 16) */
-    int64_t nblocks;         /* 2 * ceil(channels / 64) */
-    int64_t reserved2;
-    int64_t exp_ptr;         /* device int32 [nblocks]: per 32-channel-block prescale exponents written here */
-    int64_t reserved[2];
+    int64_t dst_ptr;         /* RCH_PACK_FRAGMENTS: ksteps * nblocks * 64 * frag bytes;
+                                RCH_PACK_STREAM: nblocks slabs of RCH_STREAM_SLAB_BYTES(ksteps) */
+    int64_t ksteps;          /* fragments: ceil(rank / 16); stream slabs: the kernel's rank steps (>= ceil(rank / 16)) */
+    int64_t nblocks;         /* fragments: 2 * ceil(channels / 64); stream slabs: channels / 32 */
+    int64_t kind;            /* RCH_PACK_* */
+    int64_t exp_ptr;         /* fragments: device int32 [nblocks], per 32-channel-block prescale exponents written here */
+    int64_t scale_ptr, offset_ptr; /* stream slabs: the job's fp32 [rank] affine */
 } rch_pack;                  /* 12 x int64 = 96 bytes */
+
+/* Pack kinds.  RCH_PACK_FRAGMENTS: the basis rows as MFMA A-operand fragments (every kernel but
+ * the stream kernel).  RCH_PACK_STREAM: one job's slabs for the stream kernel (RCH_GF_STREAM):
+ * per 32-channel block, W = 2^e (s_k Q_kc) as fp16 hi and lo fragments ([ksteps] x 64 lanes x
+ * 16 bytes each, hi first), the block's fp32 biases b_c = sum_k (o_k + 128 s_k) Q_kc (FP64 sum,
+ * one rounding) in channel order, and the int32 exponent e. */
+#define RCH_PACK_FRAGMENTS 0
+#define RCH_PACK_STREAM 1
+#define RCH_STREAM_SLAB_BYTES(ksteps) ((((int64_t)(ksteps)) * 2048 + 128 + 16 + 255) / 256 * 256)
 
 int rch_abi_version(void);
 int rch_job_size(void);
@@ -236,10 +258,12 @@ int rch_restore_sliced(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles
  * per device, held until the process ends) instead of memory the caller provides.  No
  * counterpart in the reference: it is for callers that cannot allocate device memory (code under
  * HIP-graph capture, tight serving loops, harnesses that forbid allocation).
- *   packs_host  host array of the group's bases (at most RCH_NOALLOC_MAX_PACKS); dst_ptr and
- *               exp_ptr are ignored: pack i's fragments go to byte
- *               F_i = sum_{j<i} round_up(ksteps_j * nblocks_j * 64 * rch_fragment_bytes(precision), 256)
- *               of the fragment region, its block exponents to word E_i = sum_{j<i} nblocks_j.
+ *   packs_host  host array of the group's packs (at most RCH_NOALLOC_MAX_PACKS); dst_ptr and
+ *               exp_ptr are ignored: pack i goes to byte F_i = sum_{j<i} round_up(size_j, 256) of the
+ *               fragment region, size = ksteps * nblocks * 64 * rch_fragment_bytes(precision) for
+ *               RCH_PACK_FRAGMENTS and nblocks * RCH_STREAM_SLAB_BYTES(ksteps) for RCH_PACK_STREAM;
+ *               fragment packs' block exponents go to word E_i = sum of nblocks over the earlier
+ *               fragment packs.
  *   jobs_dev    as for rch_restore, except that a job of pack i carries pack_ptr = F_i (relative to
  *               the fragment region) and basis_exp_index = E_i, and bound_index = -1 (no device
  *               coefficient bounds: float sources in the fp16 modes need a host bound).

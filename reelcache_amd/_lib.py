@@ -16,7 +16,7 @@ import numpy as np
 from .errors import ConfigurationError, UnsupportedError
 
 LIBRARY = Path(__file__).resolve().with_name("libreelcache_hip.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # Status codes (RCH_E_*).
 OK, E_CONFIG, E_UNSUPPORTED, E_LAUNCH = 0, 1, 2, 3
@@ -27,7 +27,8 @@ DT_F32, DT_F16, DT_BF16, DT_U8, DT_F64 = 0, 1, 2, 3, 4
 SRC_FLOAT, SRC_U8, SRC_PICTURE, SRC_DENSE = 0, 1, 2, 3
 ROPE_NONE, ROPE_SEPARABLE, ROPE_DENSE = 0, 1, 2
 JF_SRC_VEC, JF_DST_VEC, JF_ROPE_VEC = 1, 2, 4
-GF_FAST, GF_ROPE, GF_HEAD_PAIRS, GF_SPLIT_RANK = 1, 2, 4, 8
+GF_FAST, GF_ROPE, GF_HEAD_PAIRS, GF_SPLIT_RANK, GF_STREAM, GF_DENSE_ROPE = 1, 2, 4, 8, 16, 32
+STREAM_SECTION_PAIRS = 2048
 
 # rch_job field order (40 x int64).
 JOB_FIELDS = (
@@ -43,7 +44,13 @@ JOB_FIELDS = (
 )
 JOB_DTYPE = np.dtype([(name, "<i8") for name in JOB_FIELDS])
 PACK_FIELDS = ("src_ptr", "src_dtype", "row_stride", "rank", "channels", "dst_ptr", "ksteps", "nblocks",
-               "reserved2", "exp_ptr", "reserved0", "reserved1")
+               "kind", "exp_ptr", "scale_ptr", "offset_ptr")
+PACK_FRAGMENTS, PACK_STREAM = 0, 1
+
+
+def stream_slab_bytes(ksteps: int) -> int:
+    """Bytes of one (job, 32-channel block) slab of an RCH_PACK_STREAM pack."""
+    return (ksteps * 2048 + 128 + 16 + 255) // 256 * 256
 PACK_DTYPE = np.dtype([(name, "<i8") for name in PACK_FIELDS])
 # rch_fit_matrix field order (16 x int64).
 FIT_FIELDS = ("src_ptr", "src_dtype", "rows", "src_stride", "basis_ptr", "basis_stride", "rank", "coef_ptr",

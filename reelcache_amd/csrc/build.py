@@ -53,14 +53,42 @@ def _compile(hipcc: str, source: Path, verbose: bool) -> Path:
     return target
 
 
-def build(*, jobs: int | None = None, verbose: bool = False) -> Path:
-    """Compile all sources and link the shared library; returns its path."""
+def _dependencies(source: Path) -> set[Path]:
+    """The source and every header it includes with quotes, transitively."""
+    seen: set[Path] = set()
+    pending = [source]
+    while pending:
+        path = pending.pop()
+        if path in seen or not path.exists():
+            continue
+        seen.add(path)
+        for line in path.read_text().splitlines():
+            line = line.strip()
+            if line.startswith("#include \""):
+                pending.append((path.parent / line.split('"')[1]).resolve())
+    return seen
+
+
+def _stale(source: Path) -> bool:
+    target = BUILD / (source.stem + ".o")
+    if not target.exists():
+        return True
+    built = target.stat().st_mtime
+    return any(path.stat().st_mtime > built for path in _dependencies(source))
+
+
+def build(*, jobs: int | None = None, verbose: bool = False, incremental: bool = False) -> Path:
+    """Compile all sources (with ``incremental``, only those whose object is older than the
+    source or a header it includes) and link the shared library; returns its path."""
     hipcc = _hipcc()
     BUILD.mkdir(exist_ok=True)
     files = sources()
+    if incremental:
+        files = [source for source in files if _stale(source)]
     workers = max(1, min(len(files), jobs or min(8, os.cpu_count() or 1)))
     with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
-        objects = list(pool.map(lambda source: _compile(hipcc, source, verbose), files))
+        list(pool.map(lambda source: _compile(hipcc, source, verbose), files))
+    objects = [BUILD / (source.stem + ".o") for source in sources()]
     temporary = LIBRARY.with_suffix(".so.tmp")
     command = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(temporary)]
     if verbose:
@@ -73,5 +101,5 @@ def build(*, jobs: int | None = None, verbose: bool = False) -> Path:
 
 
 if __name__ == "__main__":
-    path = build(verbose="-v" in sys.argv)
+    path = build(verbose="-v" in sys.argv, incremental="--incremental" in sys.argv)
     print(path)

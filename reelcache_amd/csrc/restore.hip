@@ -6,6 +6,7 @@
 #include <mutex>
 
 #include "restore_slice.h"
+#include "restore_stream.h"
 
 namespace rch {
 namespace {
@@ -97,8 +98,106 @@ __device__ __forceinline__ float pack_max(const rch_pack& P, int dtype, int64_t 
 // undone by the restore epilogue).  Every workgroup reduces the max of its blocks itself
 // (rows are re-read from L2), so one launch suffices; its own staged rows come from the same
 // loads, so the workgroup makes one round of global reads (up to rank 256).
+// A workgroup writes the stream kernel's slabs of four 32-channel blocks of pack P (one per wave).
+// Lane (h, rho) of a wave holds channel 32 nb + block_channel(rho) and ranks 16 s + 8 h + j of
+// W = s_k Q_kc.  The block's exponent e puts max|W| in (2**13, 2**14]; 2^e W is split into fp16
+// hi + lo (the hi fragments of all steps, then the lo fragments); the bias
+// b_c = sum_k (o_k + 128 s_k) Q_kc is summed in FP64 and rounded once.  Ranks at or beyond P.rank
+// get W = 0 (the kernel multiplies arbitrary code bytes there).  The affine goes through LDS
+// (shared by the four waves); every basis load of a wave is issued before the first use.
+template <int KS, int DT>
+__device__ __forceinline__ void stream_slab_group(const rch_pack& P) {
+    __shared__ __attribute__((aligned(16))) float affine[2][16 * KS];
+    const int tid = threadIdx.x;
+    const int rank = static_cast<int>(P.rank);
+    for (int k = tid; k < 16 * KS; k += 256) {
+        affine[0][k] = k < rank ? gin<float>(P.scale_ptr)[k] : 0.0f;
+        affine[1][k] = k < rank ? gin<float>(P.offset_ptr)[k] : 0.0f;
+    }
+    __syncthreads();
+    const int64_t nb = 4 * static_cast<int64_t>(blockIdx.x) + (tid >> 6);
+    if (nb >= P.nblocks) return;
+    const int lane = tid & 63, h = lane >> 5, rho = lane & 31;
+    const int64_t c = 32 * nb + block_channel(rho);
+    const bool in = c < P.channels;
+    const int64_t stride = P.row_stride;
+    float w[KS][8];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int k = 16 * s + 8 * h + j;
+            const bool live = in && k < rank;
+            const int64_t at = live ? static_cast<int64_t>(k) * stride + c : 0;
+            float q;
+            if constexpr (DT == RCH_DT_F32) q = gin<float>(P.src_ptr)[at];
+            else if constexpr (DT == RCH_DT_F16) q = static_cast<float>(gin<_Float16>(P.src_ptr)[at]);
+            else q = static_cast<float>(gin<__bf16>(P.src_ptr)[at]);
+            w[s][j] = live ? q : 0.0f;
+        }
+    }
+    float m = 0.0f;
+    double partial = 0.0;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+        const int k0 = 16 * s + 8 * h;
+        const f4 s0 = *reinterpret_cast<const f4*>(&affine[0][k0]), s1 = *reinterpret_cast<const f4*>(&affine[0][k0 + 4]);
+        const f4 o0 = *reinterpret_cast<const f4*>(&affine[1][k0]), o1 = *reinterpret_cast<const f4*>(&affine[1][k0 + 4]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float sc = j < 4 ? s0[j] : s1[j - 4];
+            const float of = j < 4 ? o0[j] : o1[j - 4];
+            partial += (static_cast<double>(of) + 128.0 * static_cast<double>(sc)) * static_cast<double>(w[s][j]);
+            w[s][j] = __fmul_rn(sc, w[s][j]);
+            m = fmaxf(m, fabsf(w[s][j]));
+        }
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+    const int e = prescale_exponent(m);
+    const float pre = pow2f(e);
+    const int64_t slab = P.dst_ptr + nb * stream_slab_bytes(KS);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+        h8 hi, lo;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float v = __fmul_rn(w[s][j], pre);  // exact power-of-two scale
+            const _Float16 head = static_cast<_Float16>(v);
+            hi[j] = head;
+            lo[j] = static_cast<_Float16>(v - static_cast<float>(head));  // v - hi is exact
+        }
+        gout<h8>(slab)[s * 64 + lane] = hi;
+        gout<h8>(slab)[(KS + s) * 64 + lane] = lo;
+    }
+    partial += __shfl_xor(partial, 32);
+    if (h == 0) gout<float>(slab + KS * 2048)[block_channel(rho)] = static_cast<float>(partial);
+    if (lane == 0) gout<int32_t>(slab + KS * 2048 + 128)[0] = e;
+}
+
+template <int DT>
+__device__ __forceinline__ void stream_slab_steps(const rch_pack& P, int steps) {
+    switch (steps) {
+        case 4: stream_slab_group<4, DT>(P); break;
+        case 8: stream_slab_group<8, DT>(P); break;
+        case 12: stream_slab_group<12, DT>(P); break;
+        default: stream_slab_group<16, DT>(P); break;
+    }
+}
+
 template <int PREC>
 __device__ __forceinline__ void basis_pack_body(const rch_pack P) {
+    if (P.kind == RCH_PACK_STREAM) {
+        // Four blocks per workgroup, one per wave; only the y == 0 row of the grid.
+        if (blockIdx.y != 0 || 4 * static_cast<int64_t>(blockIdx.x) >= P.nblocks) return;
+        const int steps = static_cast<int>(P.ksteps);
+        switch (static_cast<int>(P.src_dtype)) {
+            case RCH_DT_F32: stream_slab_steps<RCH_DT_F32>(P, steps); break;
+            case RCH_DT_F16: stream_slab_steps<RCH_DT_F16>(P, steps); break;
+            default: stream_slab_steps<RCH_DT_BF16>(P, steps); break;
+        }
+        return;
+    }
     const int64_t nb0 = 2 * static_cast<int64_t>(blockIdx.x);
     const int64_t s0 = 2 * static_cast<int64_t>(blockIdx.y);
     if (nb0 >= P.nblocks || s0 >= P.ksteps) return;  // whole workgroup
@@ -300,10 +399,23 @@ struct Launch {
     int ks;
     bool chunked;
     int threads;  // workgroup size
+    bool stream;  // restore_stream_kernel (RCH_GF_STREAM)
 };
 
 static int pick_launch(int precision, int source_kind, int max_ksteps, int head_dim, int out_dtype, int group_flags,
                        Launch* out) {
+    if (group_flags & RCH_GF_STREAM) {
+        if (!(group_flags & RCH_GF_FAST) || (group_flags & (RCH_GF_HEAD_PAIRS | RCH_GF_SPLIT_RANK)) ||
+            precision != RCH_PREC_FP16X2 || source_kind != RCH_SRC_U8 || head_dim != 128)
+            return fail(RCH_E_CONFIG, "RCH_GF_STREAM needs RCH_GF_FAST alone, fp16x2, uint8 code rows and head_dim 128");
+        int ks = 0;
+        const int rope = !(group_flags & RCH_GF_ROPE) ? kRopeNone
+                         : ((group_flags & RCH_GF_DENSE_ROPE) ? kRopeDense : kRopeSections);
+        StreamFn fn = pick_stream_fp16x2(max_ksteps, rope, out_dtype, &ks);
+        if (!fn) return fail(RCH_E_CONFIG, "RCH_GF_STREAM: no stream variant covers %d rank steps", max_ksteps);
+        *out = {reinterpret_cast<const void*>(fn), false, ks, false, kThreads, true};
+        return RCH_OK;
+    }
     if ((group_flags & RCH_GF_FAST) && head_dim % 32 == 0 &&
         (source_kind == RCH_SRC_U8 || source_kind == RCH_SRC_PICTURE)) {
         const bool rope = (group_flags & RCH_GF_ROPE) != 0;
@@ -322,7 +434,8 @@ static int pick_launch(int precision, int source_kind, int max_ksteps, int head_
             default: break;
         }
         if (fn) {
-            *out = {reinterpret_cast<const void*>(fn), true, ks, false, shape == kRankHalves ? 2 * kThreads : kThreads};
+            *out = {reinterpret_cast<const void*>(fn), true, ks, false, shape == kRankHalves ? 2 * kThreads : kThreads,
+                    false};
             return RCH_OK;
         }
     }
@@ -339,7 +452,7 @@ static int pick_launch(int precision, int source_kind, int max_ksteps, int head_
         default: return fail(RCH_E_UNSUPPORTED, "precision %d has no matrix-core path on gfx950", precision);
     }
     if (!variant.fn) return fail(RCH_E_CONFIG, "source kind %d is not a coefficient source", source_kind);
-    *out = {reinterpret_cast<const void*>(variant.fn), false, variant.ks, variant.chunked, kThreads};
+    *out = {reinterpret_cast<const void*>(variant.fn), false, variant.ks, variant.chunked, kThreads, false};
     return RCH_OK;
 }
 
@@ -374,10 +487,14 @@ static int check_restore_args(const char* what, const rch_job* jobs_dev, int n_j
 }
 
 // Launches the kernel pick_launch chose for a group; pack_base is added to every rch_job.pack_ptr.
-static void launch_restore(const Launch& launch, const rch_job* jobs_dev, const int32_t* tiles_dev,
+static void launch_restore(const Launch& launch, const rch_job* jobs_dev, const int32_t* tiles_dev, int n_tiles,
                            const int32_t* bounds_dev, int grid, int channels, int head_dim, int out_dtype,
                            int max_ksteps, const int32_t* scratch_dev, int64_t pack_base, hipStream_t s) {
-    if (launch.fast) {
+    if (launch.stream) {
+        hipLaunchKernelGGL(reinterpret_cast<StreamFn>(const_cast<void*>(launch.fn)), dim3(static_cast<unsigned>(grid)),
+                           dim3(kThreads), 0, s, jobs_dev, tiles_dev, bounds_dev, n_tiles, channels / head_dim,
+                           pack_base);
+    } else if (launch.fast) {
         hipLaunchKernelGGL(reinterpret_cast<FastFn>(const_cast<void*>(launch.fn)), dim3(static_cast<unsigned>(grid)),
                            dim3(static_cast<unsigned>(launch.threads)), 0, s, jobs_dev, tiles_dev, bounds_dev,
                            scratch_dev, pack_base, channels / head_dim, head_dim);
@@ -399,7 +516,7 @@ int rch_restore(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev, i
     Launch launch;
     status = pick_launch(precision, source_kind, max_ksteps, head_dim, out_dtype, group_flags, &launch);
     if (status) return status;
-    launch_restore(launch, jobs_dev, tiles_dev, bounds_dev, grid, channels, head_dim, out_dtype, max_ksteps,
+    launch_restore(launch, jobs_dev, tiles_dev, n_tiles, bounds_dev, grid, channels, head_dim, out_dtype, max_ksteps,
                    scratch_dev, 0, as_stream(stream));
     return check_launch("rch_restore");
 }
@@ -530,13 +647,18 @@ int rch_restore_noalloc(const rch_pack* packs_host, int n_packs, const rch_job* 
     const int64_t fragment_base = word_base + RCH_NOALLOC_WORD_BYTES;
     for (int i = 0; i < n_packs; ++i) {
         const rch_pack& P = packs_host[i];
-        if (P.rank <= 0 || P.channels <= 0 || P.ksteps != (P.rank + 15) / 16 || P.nblocks != 2 * ((P.channels + 63) / 64))
-            return fail(RCH_E_CONFIG, "rch_restore_noalloc: pack %d: ksteps / nblocks do not match its rank / channels", i);
+        const bool slabs = P.kind == RCH_PACK_STREAM;
+        if (P.rank <= 0 || P.channels <= 0 || (P.kind != RCH_PACK_FRAGMENTS && !slabs) ||
+            (slabs ? (P.ksteps < (P.rank + 15) / 16 || P.ksteps > 16 || P.nblocks != P.channels / 32 || P.channels % 128)
+                   : (P.ksteps != (P.rank + 15) / 16 || P.nblocks != 2 * ((P.channels + 63) / 64))))
+            return fail(RCH_E_CONFIG, "rch_restore_noalloc: pack %d: kind / ksteps / nblocks do not match its rank / "
+                        "channels", i);
         args.pack[i] = P;
         args.pack[i].exp_ptr = word_base + 4 * words;
         args.pack[i].dst_ptr = fragment_base + bytes;
-        words += P.nblocks;
-        bytes += (P.ksteps * P.nblocks * 64 * fragment + 255) / 256 * 256;
+        words += slabs ? 0 : P.nblocks;
+        bytes += slabs ? P.nblocks * stream_slab_bytes(P.ksteps)
+                       : (P.ksteps * P.nblocks * 64 * fragment + 255) / 256 * 256;
         max_nblocks = P.nblocks > max_nblocks ? P.nblocks : max_nblocks;
         max_pack_steps = P.ksteps > max_pack_steps ? P.ksteps : max_pack_steps;
     }
@@ -560,7 +682,7 @@ int rch_restore_noalloc(const rch_pack* packs_host, int n_packs, const rch_job* 
     }
     status = check_launch("rch_restore_noalloc (basis pack)");
     if (status) return status;
-    launch_restore(launch, jobs_dev, tiles_dev, bounds_dev, grid, channels, head_dim, out_dtype, max_ksteps,
+    launch_restore(launch, jobs_dev, tiles_dev, n_tiles, bounds_dev, grid, channels, head_dim, out_dtype, max_ksteps,
                    reinterpret_cast<const int32_t*>(base), fragment_base, s);
     return check_launch("rch_restore_noalloc");
 }

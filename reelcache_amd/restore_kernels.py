@@ -79,7 +79,7 @@ TILE_TOKENS = 128  # tokens per workgroup tile (4 waves x 32)
 SLICE_TOKENS = 32  # tokens per tile of the channel-slice kernel (one wave's MFMA columns)
 _DEFAULT_CONFIG = {"TILE_TOKENS": TILE_TOKENS, "BLOCK_N": 32, "waves": 4, "workgroups_per_cu": None,
                    "store_cost": 4.0, "fast_variant": True, "slice_variant": False, "head_pairs": True,
-                   "split_rank": True, "static_scratch": False}
+                   "split_rank": True, "static_scratch": False, "stream_variant": False}
 # Triton tile keys the reference accepts in ``config``; they have no meaning for the HIP
 # kernels and are accepted (and ignored) so that caller configurations keep working.
 _REFERENCE_TILE_KEYS = {"BLOCK_M", "BLOCK_K", "num_warps", "num_stages", "N_GROUP", "PIC_T", "UNPACK_BLOCK_K",
@@ -1354,6 +1354,8 @@ _FAST_LIMIT = 2 ** 31
 # larger ranks run the general kernel.
 _FAST_MAX_KSTEPS = {"fp16x2": 12, "fp16": 16, "bf16": 16, "fp32": 0}
 _PAIRS_MAX_KSTEPS = 12
+_STREAM_MAX_KSTEPS = 16  # the stream kernel keeps W (both fp16 parts) of up to 256 ranks in registers
+STREAM_TOKENS = 32  # tokens per work unit of the stream kernel (csrc/restore_stream.h)
 _SPLIT_MAX_KSTEPS = 32  # rank halves (RCH_GF_SPLIT_RANK): up to 512 ranks
 
 
@@ -1448,46 +1450,134 @@ class _CallPlan:
             row[_C_PAIRS], row[_C_PAIRS_BYTES] = pairs.data_ptr(), pairs.numel() * 4
 
     def run(self, stage_events=None):
+        """Build the call's descriptors in four phases -- per-job fields, launch groups and their
+        kernel variants, basis packs, then one device buffer and the launches -- and enqueue them."""
         jobs, precision = self.jobs, self.precision
-        fragment = 32 if precision == "fp32" else 16
         fp16_mode = precision in ("fp16", "fp16x2")
         arena = _Arena()
         rows = [[0] * _N_FIELDS for _ in jobs]
         arena_refs = []  # (job index, column, arena byte offset): the field becomes buffer base + offset
-        pack_refs = []   # (job index, pack index): pack_ptr
+        affine_at = {}   # job index -> (scale, offset) arena byte offsets of its fp32 affine
+        bound_jobs = self._job_fields(rows, arena_refs, affine_at, arena, fp16_mode)
+        plans = self._launch_groups(rows, bound_jobs, arena)
+        packs, pack_of, static = self._packs(plans, affine_at, arena)
+
+        # Basis packs: sizes and offsets in the call buffer (or in the library's static array,
+        # one group at a time, for static_scratch calls).
+        fragment = 32 if precision == "fp32" else 16
+        for pack in packs:
+            pack["bytes"] = (pack["nblocks"] * _lib.stream_slab_bytes(pack["ksteps"]) if pack["kind"] == _lib.PACK_STREAM
+                             else (pack["ksteps"] * pack["nblocks"] * 64 * fragment + 255) // 256 * 256)
+        pack_total = 0
+        exp_words = 0
+        for pack in packs:
+            pack["offset"], pack["word"] = pack_total, exp_words
+            pack_total += pack["bytes"]
+            if pack["kind"] == _lib.PACK_FRAGMENTS:
+                exp_words += pack["nblocks"]
+        if static:
+            pack_total = 0
+            for plan in plans:
+                fragment_at, word_at = 0, 0
+                for index in plan.get("packs", ()):
+                    pack = packs[index]
+                    pack["static_offset"], pack["static_word"] = fragment_at, word_at
+                    fragment_at += pack["bytes"]
+                    word_at += pack["nblocks"] if pack["kind"] == _lib.PACK_FRAGMENTS else 0
+        bound_first = exp_words
+        for position, index in enumerate(bound_jobs):
+            rows[index][_C_BOUND_INDEX] = bound_first + position
+        for index, pack_index in pack_of.items():
+            pack = packs[pack_index]
+            rows[index][_C_PACK_NBLOCKS] = pack["nblocks"]
+            if static:
+                rows[index][_C_PACK_PTR], rows[index][_C_EXP_INDEX] = pack["static_offset"], pack["static_word"]
+            else:
+                rows[index][_C_EXP_INDEX] = pack["word"]
+
+        bound_tiles = _tiles(bound_jobs, jobs) if bound_jobs else None
+        bound_tile_offset = arena.add(bound_tiles) if bound_jobs else None
+        pack_desc = np.zeros(len(packs), dtype=_lib.PACK_DTYPE)
+        packs_offset = arena.reserve(pack_desc.nbytes) if packs else None
+        desc_offset = arena.reserve(len(jobs) * _N_FIELDS * 8)
+
+        # One device buffer per call: [host tables | packed bases | scratch words].
+        arena_bytes = (arena.size + 255) // 256 * 256
+        scratch_words = bound_first + len(jobs)
+        buffer = torch.empty(arena_bytes + pack_total + 4 * scratch_words + 256, dtype=torch.uint8, device=self.device)
+        base = buffer.data_ptr()
+        pack_base = base + arena_bytes
+        scratch_base = pack_base + pack_total
+        if bound_jobs:
+            start = arena_bytes + pack_total + 4 * bound_first
+            buffer[start:start + 4 * len(bound_jobs)].zero_()  # fill kernel, not a memset (graph-capture safe)
+        for index, column, offset in arena_refs:
+            rows[index][column] = base + offset
+        for position, pack in enumerate(packs):
+            entry = pack_desc[position]
+            entry["src_ptr"], entry["row_stride"], entry["channels"] = pack["src"], pack["row_stride"], pack["channels"]
+            entry["src_dtype"], entry["rank"], entry["kind"] = pack["dtype"], pack["rank"], pack["kind"]
+            entry["ksteps"], entry["nblocks"] = pack["ksteps"], pack["nblocks"]
+            entry["dst_ptr"] = pack_base + pack["offset"]
+            entry["exp_ptr"] = scratch_base + 4 * pack["word"]
+            if pack["kind"] == _lib.PACK_STREAM:
+                entry["scale_ptr"], entry["offset_ptr"] = base + pack["scale"], base + pack["offset_table"]
+        if not static:
+            for index, pack_index in pack_of.items():
+                rows[index][_C_PACK_PTR] = pack_base + packs[pack_index]["offset"]
+        if packs:
+            arena.put(packs_offset, pack_desc)
+        arena.put(desc_offset, np.array(rows, dtype=np.int64))
+        host = arena.upload(buffer)
+        self.keepalive.extend((host, buffer))
+
+        hip_stream = self.stream.cuda_stream
+        launches = 0
+        if stage_events is not None:
+            stage_events.append(("start", _record(self.stream)))
+        if packs and not static:
+            _lib.call("rch_basis_pack", base + packs_offset, len(packs), int(max(p["nblocks"] for p in packs)),
+                      int(max(p["ksteps"] for p in packs)), self.code, hip_stream)
+            launches += 1
+        if stage_events is not None:
+            stage_events.append(("pack", _record(self.stream)))
+        if bound_jobs:
+            _lib.call("rch_coefficient_bound", base + desc_offset, len(jobs), base + bound_tile_offset,
+                      len(bound_tiles), int(max(jobs[i].rank for i in bound_jobs)), scratch_base, hip_stream)
+            launches += 1
+        for plan in plans:
+            variant = plan["variant"]
+            if variant == "dense":
+                _lib.call("rch_rope_store", base + desc_offset, len(jobs), base + plan["tiles"], plan["n_tiles"],
+                          plan["channels"], plan["head_dim"], plan["out_dtype"], hip_stream)
+            elif variant == "sliced":
+                _lib.call("rch_restore_sliced", base + desc_offset, len(jobs), base + plan["tiles"], plan["n_tiles"],
+                          base + plan["entries"], plan["n_entries"], base + plan["bounds"], plan["grid"],
+                          plan["channels"], plan["head_dim"], plan["out_dtype"], self.code, plan["max_ksteps"],
+                          plan["flags"], scratch_base, hip_stream)
+            elif static:
+                host_packs = np.ascontiguousarray(pack_desc[list(plan["packs"])])
+                _lib.call("rch_restore_noalloc", host_packs.ctypes.data, len(host_packs), base + desc_offset,
+                          len(jobs), base + plan["tiles"], plan["n_tiles"], base + plan["bounds"], plan["grid"],
+                          plan["channels"], plan["head_dim"], plan["kind"], plan["out_dtype"], self.code,
+                          plan["max_ksteps"], plan["flags"], hip_stream)
+            else:
+                _lib.call("rch_restore", base + desc_offset, len(jobs), base + plan["tiles"], plan["n_tiles"],
+                          base + plan["bounds"], plan["grid"], plan["channels"], plan["head_dim"], plan["kind"],
+                          plan["out_dtype"], self.code, plan["max_ksteps"], plan["flags"], scratch_base, hip_stream)
+            launches += 1
+            if stage_events is not None:
+                stage_events.append((f"launch{launches}", _record(self.stream)))
+        if stage_events is not None:
+            stage_events.append(("fused", _record(self.stream)))
+        return launches
+
+    def _job_fields(self, rows, arena_refs, affine_at, arena, fp16_mode):
+        """Phase 1: every job's own descriptor fields and the call's fp32 affine table; returns the
+        float-source jobs whose fp16 prescale needs a device coefficient bound."""
+        jobs = self.jobs
         tables: dict = {}
-
-        # Bases: one pack per distinct basis view, covering the largest rank any job uses from it.
-        packs: dict = {}
-        basis_key = [None] * len(jobs)
-        for index, job in enumerate(jobs):
-            basis = job.basis
-            if basis is None:
-                continue
-            if basis.dtype not in BASIS_DTYPES or basis.stride(1) != 1:
-                raise ConfigurationError("GPU kernels need a float16 (or bfloat16) basis with unit column stride")
-            key = (basis.data_ptr(), basis.stride(0), basis.shape[1], basis.dtype)
-            basis_key[index] = key
-            if job.rank > packs.get(key, 0):
-                packs[key] = job.rank
-        pack_keys = list(packs)
-        n_packs = len(pack_keys)
-        pack_index = {key: index for index, key in enumerate(pack_keys)}
-        nblocks = [2 * ((key[2] + 63) // 64) for key in pack_keys]
-        ksteps = [(packs[key] + 15) // 16 for key in pack_keys]
-        pack_offsets, pack_total = [], 0
-        for blocks, steps in zip(nblocks, ksteps):
-            pack_offsets.append(pack_total)
-            pack_total += (steps * blocks * 64 * fragment + 255) // 256 * 256
-        # int32 scratch words: per-block basis exponents of every pack (written by the pack
-        # kernel), then the fp32 device coefficient bounds (one per job, zero-filled when used).
-        exp_first = [0]
-        for blocks in nblocks:
-            exp_first.append(exp_first[-1] + blocks)
-        bound_first = exp_first[-1]
-
-        affine_jobs = []  # (job index, scale, offset) of quantized / picture sources
-        bound_jobs = []
+        affine_jobs, bound_jobs = [], []
         for index, job in enumerate(jobs):
             row = rows[index]
             source = job.source
@@ -1502,11 +1592,10 @@ class _CallPlan:
                 row[_C_SRC_PTR] = values.data_ptr()
                 row[_C_SRC_ROW], row[_C_SRC_COL] = values.stride()
                 continue
+            basis = job.basis
+            if basis.dtype not in BASIS_DTYPES or basis.stride(1) != 1:
+                raise ConfigurationError("GPU kernels need a float16 (or bfloat16) basis with unit column stride")
             row[_C_RANK] = job.rank
-            pack = pack_index[basis_key[index]]
-            pack_refs.append((index, pack))
-            row[_C_PACK_NBLOCKS] = nblocks[pack]
-            row[_C_EXP_INDEX] = exp_first[pack]
             if isinstance(source, PictureSource):
                 layout = source.layout
                 pointers = [[picture.data_ptr() for picture in segment] for segment in source.pictures]
@@ -1521,21 +1610,21 @@ class _CallPlan:
                 offsets = np.array([[pointer - base for pointer in segment] for segment in pointers], dtype=np.int64)
                 arena_refs.append((index, _C_PIC_TABLE, arena.add(offsets)))
                 affine_jobs.append((index, source.scale, source.offset))
-            else:
-                values = source.values
-                row[_C_SRC_PTR] = values.data_ptr()
-                row[_C_SRC_DTYPE] = _DTYPE_CODES[values.dtype]
-                row[_C_SRC_ROW], row[_C_SRC_COL] = values.stride()
-                if source.quantized:
-                    affine_jobs.append((index, source.scale, source.offset))
-                    if values.data_ptr() % 16 == 0 and values.stride(1) == 1 and values.stride(0) % 16 == 0:
-                        row[_C_FLAGS] |= _lib.JF_SRC_VEC
-                elif fp16_mode:
-                    if source.bound is not None:
-                        row[_C_COEF_EXP] = _prescale_exponent(source.bound)
-                    else:
-                        row[_C_BOUND_INDEX] = bound_first + index
-                        bound_jobs.append(index)
+                continue
+            values = source.values
+            row[_C_SRC_PTR] = values.data_ptr()
+            row[_C_SRC_DTYPE] = _DTYPE_CODES[values.dtype]
+            row[_C_SRC_ROW], row[_C_SRC_COL] = values.stride()
+            if source.quantized:
+                affine_jobs.append((index, source.scale, source.offset))
+                if values.data_ptr() % 16 == 0 and values.stride(1) == 1 and values.stride(0) % 16 == 0:
+                    row[_C_FLAGS] |= _lib.JF_SRC_VEC
+            elif fp16_mode:
+                if source.bound is not None:
+                    row[_C_COEF_EXP] = _prescale_exponent(source.bound)
+                else:
+                    row[_C_BOUND_INDEX] = 0  # a device bound; its scratch word is assigned with the packs
+                    bound_jobs.append(index)
         if affine_jobs:
             # Every job's fp32 (scale | offset) in one host table; the fp16 modes' prescale bound
             # max(|offset|, |255 * scale + offset|) of every job in one vectorized pass.
@@ -1550,63 +1639,76 @@ class _CallPlan:
             bounds = _coefficient_bounds(scales, offsets, starts) if fp16_mode else None
             for position, (index, _, _) in enumerate(affine_jobs):
                 first = int(starts[position])
-                arena_refs.append((index, _C_SCALE, table_offset + 4 * first))
-                arena_refs.append((index, _C_OFFSET, table_offset + 4 * (total + first)))
+                at = (table_offset + 4 * first, table_offset + 4 * (total + first))
+                affine_at[index] = at
+                arena_refs.append((index, _C_SCALE, at[0]))
+                arena_refs.append((index, _C_OFFSET, at[1]))
                 if fp16_mode:
                     rows[index][_C_COEF_EXP] = _prescale_exponent(float(bounds[position]))
+        return bound_jobs
 
-        # Launch groups and their balanced persistent grids.  Jobs that qualify for the
-        # straight-line kernel (RCH_GF_FAST) are grouped apart, split by RoPE presence.
+    def _launch_groups(self, rows, bound_jobs, arena):
+        """Phase 2: launch groups (source kind, dtypes, head geometry, rank class, straight-line
+        eligibility) and the kernel variant, grid and work tables of each."""
+        jobs, precision, config = self.jobs, self.precision, self.config
+        static = bool(_config_value(config, "static_scratch"))
+        if static and bound_jobs:
+            raise ConfigurationError("static_scratch restores hold no device coefficient bounds: float sources in "
+                                     "the fp16 modes need a host bound")
+        allow_fast = bool(_config_value(config, "fast_variant"))
+        allow_slice = allow_fast and bool(_config_value(config, "slice_variant")) and not static
+        allow_pairs = allow_fast and bool(_config_value(config, "head_pairs"))
+        allow_split = bool(_config_value(config, "split_rank"))
+        allow_stream = allow_fast and bool(_config_value(config, "stream_variant")) and precision == "fp16x2"
         groups: dict = {}
-        allow_fast = bool(_config_value(self.config, "fast_variant"))
         for index, job in enumerate(jobs):
             flags = _fast_flags(rows[index], job, precision) if allow_fast else 0
             groups.setdefault(_group_key(job, precision) + (flags,), []).append(index)
         compute_units = _compute_units(self.device)
         passes = 2 if precision == "fp16x2" else (4 if precision == "fp32" else 1)
-        store_cost = float(_config_value(self.config, "store_cost"))
-        launches_planned = []
-        # static_scratch: each launch group packs its bases into the library's static device
-        # array (rch_restore_noalloc) instead of this call's buffer.
-        static = bool(_config_value(self.config, "static_scratch"))
-        if static and bound_jobs:
-            raise ConfigurationError("static_scratch restores hold no device coefficient bounds: float sources in "
-                                     "the fp16 modes need a host bound")
-        allow_slice = allow_fast and bool(_config_value(self.config, "slice_variant")) and not static
-        allow_pairs = allow_fast and bool(_config_value(self.config, "head_pairs"))
+        store_cost = float(_config_value(config, "store_cost"))
+        plans = []
         for key, members in groups.items():
             kind, group_flags = key[0], key[-1]
             first = jobs[members[0]]
             channels, head_dim = first.channels, first.destination.head_dim
-            out_dtype = _DTYPE_CODES[first.destination.tensor.dtype]
-            if kind != _lib.SRC_DENSE:
-                job_steps = {i: (jobs[i].rank + 15) // 16 for i in members}
-                max_ksteps = max(job_steps.values())
+            plan = {"kind": kind, "members": members, "channels": channels, "head_dim": head_dim,
+                    "out_dtype": _DTYPE_CODES[first.destination.tensor.dtype]}
+            plans.append(plan)
+            shape = (tuple(members), tuple(jobs[i].tokens for i in members))
+            if kind == _lib.SRC_DENSE:
+                tiles = _memo(("tiles",) + shape, lambda: _tiles(members, jobs))
+                plan.update(variant="dense", tiles=arena.add(tiles), n_tiles=len(tiles))
+                continue
+            job_steps = {i: (jobs[i].rank + 15) // 16 for i in members}
+            max_ksteps = max(job_steps.values())
+            plan["max_ksteps"] = max_ksteps
+            stream = (allow_stream and group_flags & _lib.GF_FAST and kind == _lib.SRC_U8 and head_dim == 128
+                      and channels % 128 == 0 and max_ksteps <= _STREAM_MAX_KSTEPS)
+            stream_flags = group_flags & (_lib.GF_FAST | _lib.GF_ROPE)
+            if stream and group_flags & _lib.GF_ROPE:
+                if first.rope.table.sections is None:
+                    stream_flags |= _lib.GF_DENSE_ROPE
+                elif max(_section_pairs(jobs[i]) for i in members) > _lib.STREAM_SECTION_PAIRS:
+                    stream = False  # section rows beyond the kernel's LDS table
+            if stream:
+                self._stream_plan(plan, stream_flags, compute_units, arena)
+                continue
             if allow_slice and kind == _lib.SRC_U8 and group_flags & _lib.GF_FAST:
                 head_blocks = head_dim // 32
-                blocks, slice_per_cu = _slice_blocks(self.code, max_ksteps, out_dtype, group_flags)
+                blocks, slice_per_cu = _slice_blocks(self.code, max_ksteps, plan["out_dtype"], group_flags)
                 per_slice = _slice_heads(blocks, head_blocks)
                 if per_slice >= 1 and slice_per_cu >= 1:
                     slice_grid = compute_units * slice_per_cu
-                    member_packs = [pack_index[basis_key[i]] for i in members]
-                    tiles, entries, wg_entries = _slice_plan(members, jobs, member_packs, ksteps,
-                                                             channels // head_dim, head_blocks, per_slice, slice_grid)
-                    launches_planned.append(("sliced", arena.add(tiles), len(tiles), arena.add(entries), len(entries),
-                                             arena.add(wg_entries), slice_grid, channels, head_dim, out_dtype,
-                                             max_ksteps, group_flags))
+                    plan["pending_slice"] = (group_flags, head_blocks, per_slice, slice_grid)
+                    plan.update(variant="sliced", flags=group_flags, grid=slice_grid)
                     self.grids.append(slice_grid)
                     self.variants.append("sliced")
                     continue
-            shape = (tuple(members), tuple(jobs[i].tokens for i in members))
             tiles = _memo(("tiles",) + shape, lambda: _tiles(members, jobs))
-            tile_offset = arena.add(tiles)
-            if kind == _lib.SRC_DENSE:
-                launches_planned.append(("dense", tile_offset, len(tiles), channels, head_dim, out_dtype))
-                continue
             if group_flags & _lib.GF_FAST and max_ksteps > _FAST_MAX_KSTEPS[precision]:
                 # Beyond one wave's registers: rank halves in 8-wave workgroups (uint8 rows, up to
                 # 32 rank steps), else the general kernel.
-                allow_split = bool(_config_value(self.config, "split_rank"))
                 if allow_split and kind == _lib.SRC_U8 and max_ksteps <= _SPLIT_MAX_KSTEPS:
                     group_flags = (group_flags & ~_lib.GF_HEAD_PAIRS) | _lib.GF_SPLIT_RANK
                 else:
@@ -1615,8 +1717,8 @@ class _CallPlan:
                     and (channels // head_dim) % 2 == 0 and max_ksteps <= _PAIRS_MAX_KSTEPS):
                 group_flags |= _lib.GF_HEAD_PAIRS  # a work unit: one dim block of two heads
             blocks_per_tile = (channels + 31) // 32 // (2 if group_flags & _lib.GF_HEAD_PAIRS else 1)
-            per_cu = self.config.get("workgroups_per_cu") or _occupancy(self.code, kind, max_ksteps, head_dim, out_dtype,
-                                                                        group_flags)
+            per_cu = config.get("workgroups_per_cu") or _occupancy(self.code, kind, max_ksteps, head_dim,
+                                                                   plan["out_dtype"], group_flags)
             grid = int(max(1, min(len(tiles) * blocks_per_tile, compute_units * max(1, per_cu))))
 
             def balanced():
@@ -1624,105 +1726,87 @@ class _CallPlan:
                 return _balanced_bounds(steps * passes + store_cost, blocks_per_tile, grid)
             bounds = _memo(("bounds",) + shape + (tuple(job_steps[i] for i in members), blocks_per_tile, grid, passes,
                                                   store_cost), balanced)
-            group_packs = None
-            if static:
-                # The documented layout of rch_restore_noalloc: pack i of the group at fragment byte
-                # F_i and exponent word E_i (sums over the group's earlier packs).
-                group_packs = list(dict.fromkeys(pack_index[basis_key[i]] for i in members))
-                placed, fragment_at, word_at = {}, 0, 0
-                for pack in group_packs:
-                    placed[pack] = (fragment_at, word_at)
-                    fragment_at += (ksteps[pack] * nblocks[pack] * 64 * fragment + 255) // 256 * 256
-                    word_at += nblocks[pack]
-                for i in members:
-                    rows[i][_C_PACK_PTR], rows[i][_C_EXP_INDEX] = placed[pack_index[basis_key[i]]]
-            launches_planned.append(("restore", tile_offset, len(tiles), arena.add(bounds), grid, channels, head_dim,
-                                     kind, out_dtype, max_ksteps, group_flags, group_packs))
+            plan.update(variant="general" if not group_flags & _lib.GF_FAST
+                        else ("pairs" if group_flags & _lib.GF_HEAD_PAIRS
+                              else ("split" if group_flags & _lib.GF_SPLIT_RANK else "fast")),
+                        tiles=arena.add(tiles), n_tiles=len(tiles), bounds=arena.add(bounds), grid=grid,
+                        flags=group_flags)
             self.grids.append(grid)
-            self.variants.append("general" if not group_flags & _lib.GF_FAST
-                                 else ("pairs" if group_flags & _lib.GF_HEAD_PAIRS
-                                       else ("split" if group_flags & _lib.GF_SPLIT_RANK else "fast")))
-        bound_tiles = _tiles(bound_jobs, jobs) if bound_jobs else None
-        bound_tile_offset = arena.add(bound_tiles) if bound_jobs else None
-        pack_desc = np.zeros(n_packs, dtype=_lib.PACK_DTYPE)
-        packs_offset = arena.reserve(pack_desc.nbytes) if n_packs else None
-        desc_offset = arena.reserve(len(jobs) * _N_FIELDS * 8)
+            self.variants.append(plan["variant"])
+        return plans
 
-        # One device buffer per call: [host tables | packed bases | scratch words].
-        arena_bytes = (arena.size + 255) // 256 * 256
-        if static:
-            pack_total = 0  # the packs live in the library's static array
-        scratch_words = bound_first + len(jobs)
-        buffer = torch.empty(arena_bytes + pack_total + 4 * scratch_words + 256, dtype=torch.uint8, device=self.device)
-        base = buffer.data_ptr()
-        pack_base = base + arena_bytes
-        scratch_base = pack_base + pack_total
-        if bound_jobs:
-            start = arena_bytes + pack_total + 4 * bound_first
-            buffer[start:start + 4 * len(jobs)].zero_()  # fill kernel, not a memset (graph-capture safe)
-        for index, key in enumerate(pack_keys):
-            entry = pack_desc[index]
-            entry["src_ptr"], entry["row_stride"], entry["channels"] = key[0], key[1], key[2]
-            entry["src_dtype"] = _DTYPE_CODES[key[3]]
-            entry["rank"] = packs[key]
-            entry["dst_ptr"] = pack_base + pack_offsets[index]
-            entry["ksteps"] = ksteps[index]
-            entry["nblocks"] = nblocks[index]
-            entry["exp_ptr"] = scratch_base + 4 * exp_first[index]
-        for index, column, offset in arena_refs:
-            rows[index][column] = base + offset
-        if not static:
-            for index, pack in pack_refs:
-                rows[index][_C_PACK_PTR] = pack_base + pack_offsets[pack]
-        if n_packs:
-            arena.put(packs_offset, pack_desc)
-        arena.put(desc_offset, np.array(rows, dtype=np.int64))
-        host = arena.upload(buffer)
-        self.keepalive.extend((host, buffer))
+    def _stream_plan(self, plan, group_flags, compute_units, arena):
+        """Work tables of a stream-kernel group: units (job, head, 32-token tile) job-major, and an
+        equal split of them over the resident workgroups."""
+        jobs, members = self.jobs, plan["members"]
+        heads = plan["channels"] // 128
+        flags = group_flags | _lib.GF_STREAM
+        units = [heads * ((jobs[i].tokens + STREAM_TOKENS - 1) // STREAM_TOKENS) for i in members]
+        table = np.zeros((len(members) + 1, 2), dtype=np.int32)
+        table[1:, 0] = np.cumsum(units)
+        table[:-1, 1] = members
+        total = int(table[-1, 0])
+        per_cu = self.config.get("workgroups_per_cu") or _occupancy(self.code, _lib.SRC_U8, plan["max_ksteps"], 128,
+                                                                    plan["out_dtype"], flags)
+        grid = int(max(1, min(total, compute_units * max(1, per_cu))))
+        bounds = (np.arange(grid + 1, dtype=np.int64) * total // grid).astype(np.int32)
+        plan.update(variant="stream", flags=flags, tiles=arena.add(table), n_tiles=len(members),
+                    bounds=arena.add(bounds), grid=grid,
+                    stream_ksteps=next(size for size in (4, 8, 12, 16) if plan["max_ksteps"] <= size))
+        self.grids.append(grid)
+        self.variants.append("stream")
 
-        hip_stream = self.stream.cuda_stream
-        launches = 0
-        if stage_events is not None:
-            stage_events.append(("start", _record(self.stream)))
-        if n_packs and not static:
-            _lib.call("rch_basis_pack", base + packs_offset, n_packs, int(max(nblocks)), int(max(ksteps)), self.code,
-                      hip_stream)
-            launches += 1
-        if stage_events is not None:
-            stage_events.append(("pack", _record(self.stream)))
-        if bound_jobs:
-            _lib.call("rch_coefficient_bound", base + desc_offset, len(jobs), base + bound_tile_offset,
-                      len(bound_tiles), int(max(jobs[i].rank for i in bound_jobs)), scratch_base, hip_stream)
-            launches += 1
-        for plan in launches_planned:
-            if plan[0] == "dense":
-                _, tile_offset, n_tiles, channels, head_dim, out_dtype = plan
-                _lib.call("rch_rope_store", base + desc_offset, len(jobs), base + tile_offset, n_tiles, channels,
-                          head_dim, out_dtype, hip_stream)
-            elif plan[0] == "sliced":
-                (_, tile_offset, n_tiles, entries_offset, n_entries, wg_offset, grid, channels, head_dim, out_dtype,
-                 max_ksteps, group_flags) = plan
-                _lib.call("rch_restore_sliced", base + desc_offset, len(jobs), base + tile_offset, n_tiles,
-                          base + entries_offset, n_entries, base + wg_offset, grid, channels, head_dim, out_dtype,
-                          self.code, max_ksteps, group_flags, scratch_base, hip_stream)
-            else:
-                (_, tile_offset, n_tiles, bounds_offset, grid, channels, head_dim, kind, out_dtype, max_ksteps,
-                 group_flags, group_packs) = plan
-                if group_packs is None:
-                    _lib.call("rch_restore", base + desc_offset, len(jobs), base + tile_offset, n_tiles,
-                              base + bounds_offset, grid, channels, head_dim, kind, out_dtype, self.code, max_ksteps,
-                              group_flags, scratch_base, hip_stream)
-                else:
-                    host_packs = np.ascontiguousarray(pack_desc[group_packs])
-                    _lib.call("rch_restore_noalloc", host_packs.ctypes.data, len(group_packs), base + desc_offset,
-                              len(jobs), base + tile_offset, n_tiles, base + bounds_offset, grid, channels, head_dim,
-                              kind, out_dtype, self.code, max_ksteps, group_flags, hip_stream)
-            launches += 1
-            if stage_events is not None:
-                stage_events.append((f"launch{launches}", _record(self.stream)))
-        if stage_events is not None:
-            stage_events.append(("fused", _record(self.stream)))
-        return launches
+    def _packs(self, plans, affine_at, arena):
+        """Phase 3: the basis packs of the call -- one per job of a stream group (its scaled slabs),
+        one per distinct basis view for the other kernels (fragments of the largest rank used) --
+        and the pending work tables of channel-slice groups, which index packs."""
+        jobs = self.jobs
+        static = bool(_config_value(self.config, "static_scratch"))
+        packs: list = []
+        pack_of: dict = {}
+        by_basis: dict = {}
+        for plan in plans:
+            if plan["variant"] == "dense":
+                continue
+            used = []
+            for index in plan["members"]:
+                job = jobs[index]
+                basis = job.basis
+                if plan["variant"] == "stream":
+                    packs.append({"kind": _lib.PACK_STREAM, "src": basis.data_ptr(), "row_stride": basis.stride(0),
+                                  "channels": basis.shape[1], "dtype": _DTYPE_CODES[basis.dtype], "rank": job.rank,
+                                  "ksteps": plan["stream_ksteps"], "nblocks": basis.shape[1] // 32,
+                                  "scale": affine_at[index][0], "offset_table": affine_at[index][1]})
+                    pack_of[index] = len(packs) - 1
+                    used.append(len(packs) - 1)
+                    continue
+                key = (basis.data_ptr(), basis.stride(0), basis.shape[1], basis.dtype)
+                position = by_basis.get(key)
+                if position is None:
+                    position = by_basis[key] = len(packs)
+                    packs.append({"kind": _lib.PACK_FRAGMENTS, "src": key[0], "row_stride": key[1], "channels": key[2],
+                                  "dtype": _DTYPE_CODES[key[3]], "rank": 0, "nblocks": 2 * ((key[2] + 63) // 64)})
+                packs[position]["rank"] = max(packs[position]["rank"], job.rank)
+                pack_of[index] = position
+                if position not in used:
+                    used.append(position)
+            plan["packs"] = used
+        for pack in packs:
+            if pack["kind"] == _lib.PACK_FRAGMENTS:
+                pack["ksteps"] = (pack["rank"] + 15) // 16
+        for plan in plans:
+            pending = plan.pop("pending_slice", None)
+            if pending is None:
+                continue
+            group_flags, head_blocks, per_slice, slice_grid = pending
+            members = plan["members"]
+            ksteps = [pack["ksteps"] for pack in packs]
+            tiles, entries, wg_entries = _slice_plan(members, jobs, [pack_of[i] for i in members], ksteps,
+                                                     plan["channels"] // plan["head_dim"], head_blocks, per_slice,
+                                                     slice_grid)
+            plan.update(tiles=arena.add(tiles), n_tiles=len(tiles), entries=arena.add(entries),
+                        n_entries=len(entries), bounds=arena.add(wg_entries))
+        return packs, pack_of, static
 
 
 def _record(stream):
@@ -1747,8 +1831,17 @@ def _rank_class(precision, job):
 
 def _group_key(job, precision=None):
     kind, dtype = _source_kind(job)
+    rope = None if job.rope is None else job.rope.table.sections is None  # dense tables apart from separable
     return (kind, dtype, job.destination.tensor.dtype, job.destination.head_dim, job.channels,
-            _rank_class(precision, job) if precision is not None else 0)
+            _rank_class(precision, job) if precision is not None else 0, rope)
+
+
+def _section_pairs(job):
+    """(cos, sin) pairs of a separable table that the stream kernel stages in LDS for a job: every
+    row of each section the job's grid can reach."""
+    sections = job.rope.table.sections
+    frames, height, width = job.grid
+    return frames * sections[0] + height * sections[1] + width * sections[2]
 
 
 def _resolve_backend(backend, cuda):

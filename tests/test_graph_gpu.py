@@ -1,7 +1,7 @@
 """GPU test of restores captured in a HIP graph.
 
-A call of K (RoPE) and V jobs is captured once per kernel variant (straight-line with two or one
-heads per step or rank halves, channel-slice, general); the graph is replayed several times, with eager work and synchronizations between the
+A call of K (RoPE) and V jobs is captured once per kernel variant (stream, straight-line with two
+or one heads per step or rank halves, channel-slice, general); the graph is replayed several times, with eager work and synchronizations between the
 replays and the destinations overwritten before each, and every replay must reproduce the eager
 result bit for bit.  Captured calls take their descriptor staging from memory reserved
 beforehand (``reserve_capture_staging``); the capture itself allocates no pinned memory and
@@ -39,7 +39,10 @@ def _jobs(device, ranks=(96, 160)):
 
 @pytest.mark.parametrize("config,ranks", [({}, (96, 160)), ({"head_pairs": False}, (96, 160)),
                                           ({"slice_variant": True}, (96, 160)), ({"fast_variant": False}, (96, 160)),
-                                          ({}, (256, 448))])  # rank halves (8-wave workgroups)
+                                          ({}, (256, 448)),  # rank halves (8-wave workgroups)
+                                          ({"stream_variant": True}, (96, 160)),  # the stream kernel
+                                          ({"stream_variant": True, "static_scratch": True}, (96, 160)),
+                                          ({"stream_variant": True}, (256, 448))])  # stream (256), rank halves (448)
 def test_captured_restore_replays_match_eager(device, config, ranks):
     jobs, caches = _jobs(device, ranks)
     for cache in caches:
