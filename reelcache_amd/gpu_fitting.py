@@ -2,16 +2,18 @@
 
 Public surface of ``reelcache/gpu_fitting.py``: GPU_FIT_METHODS, EIGH_SOLVERS, BoundedEigh
 (:100-235), select_eigh_solver (:238-273), gram_bases (:276-295) and GPUFitter (:298-522) with
-``prefit`` / ``fit`` / ``plan_chunk`` / ``adopt_current_thread`` / ``clear_prefit``.
+``prefit`` / ``fit`` / ``plan_chunk`` / ``adopt_current_thread`` / ``clear_prefit``; the record
+and metrics keys are that interface.
 
 MI355X design:
 * the Gram of every source is one launch of the hand-written HIP kernel (``rch_fit_gram``:
   exact 16-bit products on MFMA, fp32 accumulation, only lower-triangle tiles computed,
   written exactly symmetric, so the reference's ``(G + G^T) / 2`` is the identity);
 * the batched symmetric eigensolve is rocSOLVER through ``torch.linalg.eigh`` on the stacked
-  batch (ascending values, columns transposed to rows), sub-batched by :class:`BoundedEigh`
-  exactly as the reference sub-batches cuSOLVER; cuSOLVER's ctypes binding does not exist on
-  ROCm and is refused loudly;
+  batch (ascending values, columns transposed to rows).  :class:`BoundedEigh` schedules it: a
+  fixed sub-batch pads the batch's tail with identity matrices once and solves equal chunks; a
+  memory- or solver-bounded batch takes the first size of its halving sequence that fits.
+  cuSOLVER's ctypes binding does not exist on ROCm and is refused loudly;
 * projection, residual and source energies are the FP64-MFMA kernels of
   :mod:`reelcache_amd.factorization`.
 
@@ -24,10 +26,12 @@ import contextlib
 import os
 import threading
 import time
+from typing import NamedTuple
 
 import torch
 
 from . import fit_kernels
+from ._checks import need
 from .errors import CapacityError, ConfigurationError, StateError, UnsupportedError
 from .factorization import (
     Factors, _canonical_signs, all_finite, fast_condition_bound, project_onto_basis, validate_matrix, validate_rank,
@@ -49,10 +53,12 @@ PER_MATRIX_EIGH_MIN_N = 4096
 
 
 def _torch_version() -> tuple[int, int]:
-    head = torch.__version__.split("+")[0].split(".")
+    """(major, minor) of the running Torch."""
+    release = torch.__version__.partition("+")[0]
     try:
-        return int(head[0]), int(head[1])
-    except (IndexError, ValueError) as error:
+        major, minor = release.split(".")[:2]
+        return int(major), int(minor)
+    except ValueError as error:
         raise UnsupportedError(f"cannot parse the running Torch version {torch.__version__!r}") from error
 
 
@@ -67,13 +73,15 @@ def torch_batched_eigh_is_rocsolver() -> bool:
 
 
 def _torch_rows_eigh(grams):
+    """Stacked eigh: ascending values and eigenvectors as rows."""
     values, columns = torch.linalg.eigh(grams)
-    return values, columns.transpose(1, 2)
+    return values, columns.mT
 
 
 def _torch_loop_eigh(grams):
-    pairs = [torch.linalg.eigh(gram) for gram in grams]
-    return torch.stack([values for values, _ in pairs]), torch.stack([columns.T for _, columns in pairs])
+    """One eigh per matrix (the explicit diagnostic solver), stacked like :func:`_torch_rows_eigh`."""
+    solved = [_torch_rows_eigh(gram[None]) for gram in grams]
+    return torch.cat([values for values, _ in solved]), torch.cat([rows for _, rows in solved])
 
 
 def default_eigh_sub_batch(n: int) -> int | None:
@@ -84,6 +92,25 @@ def default_eigh_sub_batch(n: int) -> int | None:
 def xsyevbatched_workspace_bytes(batch: int, n: int, device) -> int | None:
     """cuSOLVER's workspace query; there is no cuSOLVER on ROCm."""
     raise UnsupportedError("the cusolverDnXsyevBatched buffer-size query needs CUDA's cuSOLVER (absent on ROCm)")
+
+
+class _Schedule(NamedTuple):
+    """How one batch is solved: chunks of ``size`` matrices, why, and whether the size exceeds the
+    memory bound (a fixed sub-batch, or one matrix that still does not fit)."""
+
+    size: int
+    reason: str
+    over_budget: bool = False
+
+
+def _halvings(batch):
+    """batch, ceil(batch / 2), ... down to 1."""
+    size = batch
+    while True:
+        yield size
+        if size == 1:
+            return
+        size = (size + 1) // 2
 
 
 class BoundedEigh:
@@ -102,104 +129,101 @@ class BoundedEigh:
 
     def __init__(self, label: str, solver, *, memory_fraction: float = EIGH_MEMORY_FRACTION, workspace=None,
                  total_memory: int | None = None, sub_batch_size=None):
-        if not 0 < memory_fraction <= 1:
-            raise ConfigurationError("eigh memory fraction must be in (0, 1]")
-        if total_memory is not None and (type(total_memory) is not int or total_memory <= 0):
-            raise ConfigurationError("total_memory must be a positive byte count")
-        if sub_batch_size is not None and not callable(sub_batch_size):
-            raise ConfigurationError("sub_batch_size must map n to a fixed sub-batch size or None")
-        self.label, self.solver, self.memory_fraction = label, solver, memory_fraction
+        need(0 < memory_fraction <= 1, "eigh memory fraction must be in (0, 1]")
+        need(total_memory is None or (type(total_memory) is int and total_memory > 0),
+             "total_memory must be a positive byte count")
+        need(sub_batch_size is None or callable(sub_batch_size),
+             "sub_batch_size must map n to a fixed sub-batch size or None")
+        self.label, self.solver = label, solver
+        self.memory_fraction, self.total_memory = memory_fraction, total_memory
         self._workspace = workspace  # (batch, n, device) -> bytes, or None when the solver rejects the size
-        self.total_memory = total_memory
-        self.sub_batch_size = default_eigh_sub_batch if sub_batch_size is None else sub_batch_size
+        self.sub_batch_size = sub_batch_size or default_eigh_sub_batch
         self.calls: list[dict] = []
         self.last: dict | None = None
 
     def derive(self, *, memory_fraction: float | None = None, total_memory: int | None = None) -> "BoundedEigh":
         """The same solver and sub-batch policy under another memory bound."""
-        return BoundedEigh(self.label, self.solver,
-                           memory_fraction=self.memory_fraction if memory_fraction is None else memory_fraction,
-                           workspace=self._workspace, total_memory=total_memory, sub_batch_size=self.sub_batch_size)
+        fraction = self.memory_fraction if memory_fraction is None else memory_fraction
+        return BoundedEigh(self.label, self.solver, memory_fraction=fraction, workspace=self._workspace,
+                           total_memory=total_memory, sub_batch_size=self.sub_batch_size)
 
-    def _workspace_bytes(self, batch: int, n: int, device) -> int | None:
+    def _workspace_bytes(self, size: int, n: int, device) -> int | None:
         if self._workspace is not None:
-            return self._workspace(batch, n, device)
-        return None if batch * n * n > EIGH_UNQUERIED_ELEMENT_LIMIT else 4 * batch * n * n
+            return self._workspace(size, n, device)
+        elements = size * n * n
+        return None if elements > EIGH_UNQUERIED_ELEMENT_LIMIT else 4 * elements
 
     def _budget(self, device) -> float | None:
-        if self.total_memory is None and device.type != "cuda":
+        """Bytes one solver call may use; None (unbounded) for host solves without a stated total."""
+        if self.total_memory is not None:
+            return self.memory_fraction * self.total_memory
+        if device.type != "cuda":
             return None
-        total = self.total_memory or torch.cuda.get_device_properties(device).total_memory
-        return self.memory_fraction * total
+        return self.memory_fraction * torch.cuda.get_device_properties(device).total_memory
 
     @staticmethod
     def _need(size: int, n: int, workspace: int) -> int:
-        return 8 * size * n * n + 4 * size * n + workspace  # input copy + vectors, values, workspace
+        """Input copy and eigenvectors (2 x 4 bytes per element), values, and the solver workspace."""
+        return size * n * (8 * n + 4) + workspace
+
+    def _fits(self, size, n, device, budget):
+        """(reason the size fails, or None when it fits; its workspace bytes)."""
+        workspace = self._workspace_bytes(size, n, device)
+        if workspace is None:
+            return "solver_rejects_batch_size", None
+        if budget is not None and self._need(size, n, workspace) > budget:
+            return "memory_bound", workspace
+        return None, workspace
 
     def sub_batch(self, batch: int, n: int, device) -> tuple[int, str]:
-        return self._sub_batch(batch, n, device)[:2]
+        return tuple(self._schedule(batch, n, device)[:2])
 
-    def _sub_batch(self, batch: int, n: int, device) -> tuple[int, str, bool]:
+    def _schedule(self, batch: int, n: int, device) -> _Schedule:
         device = torch.device(device)
-        fixed = self.sub_batch_size(n)
         budget = self._budget(device)
+        fixed = self.sub_batch_size(n)
         if fixed is not None:
-            if type(fixed) is not int or fixed < 1:
-                raise ConfigurationError(f"sub_batch_size({n}) must be a positive integer or None")
+            need(type(fixed) is int and fixed >= 1, f"sub_batch_size({n}) must be a positive integer or None")
             reason = "per_matrix" if fixed == 1 else "fixed_sub_batch"
             if budget is None:
-                return fixed, reason, False
-            workspace = self._workspace_bytes(fixed, n, device)
-            if workspace is None:
-                raise UnsupportedError(f"the batched eigensolver rejects the fixed sub-batch of {fixed} {n}x{n} matrices")
-            return fixed, reason, self._need(fixed, n, workspace) > budget
+                return _Schedule(fixed, reason)
+            failure, _ = self._fits(fixed, n, device, budget)
+            need(failure != "solver_rejects_batch_size",
+                 f"the batched eigensolver rejects the fixed sub-batch of {fixed} {n}x{n} matrices", UnsupportedError)
+            return _Schedule(fixed, reason, failure is not None)
         if budget is None:
-            return batch, "whole_batch", False
-        size, reason = batch, "whole_batch"
-        while True:
-            workspace = self._workspace_bytes(size, n, device)
-            if workspace is None:
-                reason = "solver_rejects_batch_size"
-            elif self._need(size, n, workspace) > budget:
-                reason = "memory_bound"
-            else:
-                return size, reason, False
-            if size == 1:
-                if workspace is None:
-                    raise UnsupportedError(f"the batched eigensolver rejects even one {n}x{n} matrix")
-                return 1, reason, True
-            size = (size + 1) // 2
+            return _Schedule(batch, "whole_batch")
+        reason = "whole_batch"
+        for size in _halvings(batch):
+            failure, _ = self._fits(size, n, device, budget)
+            if failure is None:
+                return _Schedule(size, reason)
+            reason = failure
+        need(failure != "solver_rejects_batch_size", f"the batched eigensolver rejects even one {n}x{n} matrix",
+             UnsupportedError)
+        return _Schedule(1, reason, True)
 
     def __call__(self, grams: torch.Tensor):
         batch, n = int(grams.shape[0]), int(grams.shape[1])
-        size, reason, over_budget = self._sub_batch(batch, n, grams.device)
-        fixed = reason in ("per_matrix", "fixed_sub_batch")
-        padded = 0
-        if size == batch:
+        plan = self._schedule(batch, n, grams.device)
+        fixed = plan.reason in ("per_matrix", "fixed_sub_batch")
+        padding = (-batch) % plan.size if fixed else 0
+        if padding:
+            identities = torch.eye(n, dtype=grams.dtype, device=grams.device).expand(padding, n, n)
+            grams = torch.cat((grams, identities))
+        if plan.size >= grams.shape[0]:
             values, vectors = self.solver(grams)
         else:
-            values = vectors = None
-            for start in range(0, batch, size):
-                part = grams[start:start + size]
-                count = int(part.shape[0])
-                if fixed and count < size:
-                    padded = size - count
-                    identity = torch.eye(n, dtype=grams.dtype, device=grams.device).expand(padded, n, n)
-                    part = torch.cat((part, identity))
-                part_values, part_vectors = self.solver(part.contiguous())
-                if values is None:
-                    values = part_values.new_empty((batch, *part_values.shape[1:]))
-                    vectors = part_vectors.new_empty((batch, *part_vectors.shape[1:]))
-                values[start:start + count] = part_values[:count]
-                vectors[start:start + count] = part_vectors[:count]
-        record = {"batch": batch, "n": n, "sub_batch": size if fixed else min(size, batch),
-                  "solver_calls": -(-batch // size), "reason": reason}
-        if padded:
-            record["padded"] = padded
-        if over_budget:
-            record["over_budget"] = True
-        self.last = record
+            parts = [self.solver(chunk.contiguous()) for chunk in torch.split(grams, plan.size)]
+            values, vectors = (torch.cat([part[i] for part in parts]) for i in (0, 1))
+        if padding:
+            values, vectors = values[:batch], vectors[:batch]
+        record = {"batch": batch, "n": n, "sub_batch": plan.size if fixed else min(plan.size, batch),
+                  "solver_calls": -(-batch // plan.size), "reason": plan.reason}
+        record.update({"padded": padding} if padding else {})
+        record.update({"over_budget": True} if plan.over_budget else {})
         self.calls.append(record)
+        self.last = record
         return values, vectors
 
 
@@ -211,20 +235,17 @@ def select_eigh_solver(solver="auto", *, sub_batch_size=None):
     UnsupportedError (no cuSOLVER on ROCm).  ``torch_loop`` is the explicit per-matrix
     diagnostic.  ``eigh`` maps ``[b, n, n]`` to ascending values and row eigenvectors.
     """
-    if solver not in EIGH_SOLVERS:
-        raise ConfigurationError(f"eigh solver must be one of {EIGH_SOLVERS}")
-    if solver in ("auto", "torch_batched"):
-        if torch_batched_eigh_is_rocsolver():
-            label = "torch_linalg_eigh_batched_rocsolver"
+    need(solver in EIGH_SOLVERS, f"eigh solver must be one of {EIGH_SOLVERS}")
+    if solver == "torch_loop":
+        return "torch_eigh_loop_explicit", _torch_loop_eigh
+    need(solver != "cusolver_ctypes", "the ctypes cusolverDnXsyevBatched binding needs CUDA's cuSOLVER, which ROCm "
+         "does not provide; use eigh_solver='auto' (rocSOLVER)", UnsupportedError)
+    for backend, available in (("rocsolver", torch_batched_eigh_is_rocsolver),
+                               ("xsyevbatched", torch_batched_eigh_is_xsyevbatched)):
+        if available():
+            label = f"torch_linalg_eigh_batched_{backend}"
             return label, BoundedEigh(label, _torch_rows_eigh, sub_batch_size=sub_batch_size)
-        if torch_batched_eigh_is_xsyevbatched():
-            label = "torch_linalg_eigh_batched_xsyevbatched"
-            return label, BoundedEigh(label, _torch_rows_eigh, sub_batch_size=sub_batch_size)
-        raise UnsupportedError(f"Torch {torch.__version__} has no batched device eigensolver for this build")
-    if solver == "cusolver_ctypes":
-        raise UnsupportedError("the ctypes cusolverDnXsyevBatched binding needs CUDA's cuSOLVER, which ROCm does not "
-                               "provide; use eigh_solver='auto' (rocSOLVER)")
-    return "torch_eigh_loop_explicit", _torch_loop_eigh
+    raise UnsupportedError(f"Torch {torch.__version__} has no batched device eigensolver for this build")
 
 
 def gram_bases(sources, ranks, *, eigh=None):
@@ -234,62 +255,80 @@ def gram_bases(sources, ranks, *, eigh=None):
     The Grams are one launch of the MFMA Gram kernel; ``eigh`` maps ``[b, n, n]`` to
     ``(values, row_vectors)`` (default: ``torch.linalg.eigh``, columns transposed to rows).
     """
-    if not sources or len(sources) != len(ranks):
-        raise ConfigurationError("batched Gram fitting needs one rank per source")
-    if len({int(x.shape[1]) for x in sources}) != 1:
-        raise ConfigurationError("one Gram batch must share the channel count")
-    grams = fit_kernels.gram(list(sources))
-    if eigh is None:
-        _, columns = torch.linalg.eigh(grams)
-        vectors = columns.transpose(1, 2)
-    else:
-        _, vectors = eigh(grams)
-    return [vectors[index, -rank:].flip(0) for index, rank in enumerate(ranks)]
+    need(sources and len(sources) == len(ranks), "batched Gram fitting needs one rank per source")
+    need(len({int(x.shape[1]) for x in sources}) == 1, "one Gram batch must share the channel count")
+    _, rows = (eigh or _torch_rows_eigh)(fit_kernels.gram(list(sources)))
+    # Ascending eigenvalues: the top-rank rows are the last ones, reversed into descending energy.
+    return [rows[index, -rank:].flip(0) for index, rank in enumerate(ranks)]
 
 
 def _stored_bases(bases) -> list[torch.Tensor]:
     """Canonical signs, FP16 rounding, and one finiteness read for the whole group."""
     stored = [_canonical_signs(basis).to(dtype=torch.float16).contiguous() for basis in bases]
     finite = torch.stack([torch.isfinite(basis).all() for basis in stored]).cpu()
-    if not bool(finite.all()):
-        raise ConfigurationError("fitted basis is not finite in stored FP16")
+    need(bool(finite.all()), "fitted basis is not finite in stored FP16")
     return stored
 
 
+def _fitter_rules(gpu_id, gpu_uuid, method, max_workspace_bytes, seed, power_iterations, batch_size, side_stream,
+                  shared, eigh_solver):
+    """``(holds, message)`` rules of the :class:`GPUFitter` options, in order."""
+    yield (type(gpu_id) is int and gpu_id >= 0 and isinstance(gpu_uuid, str) and gpu_uuid.startswith("GPU-"),
+           "GPU fitting requires an explicit visible device index and UUID")
+    yield method in GPU_FIT_METHODS, "unsupported GPU fitting backend"
+    yield type(max_workspace_bytes) is int and max_workspace_bytes > 0, "GPU fitting workspace budget must be positive"
+    yield (type(seed) is int and seed >= 0 and type(power_iterations) is int and 0 <= power_iterations <= 8,
+           "invalid GPU fitting seed or iteration count")
+    yield type(batch_size) is int and 1 <= batch_size <= 256, "GPU fitting batch size must be an integer in [1, 256]"
+    yield type(side_stream) is bool, "side_stream must be boolean"
+    yield type(shared) is bool, "shared must be boolean"
+    yield eigh_solver in EIGH_SOLVERS, f"eigh_solver must be one of {EIGH_SOLVERS}"
+
+
+def _tensor_identity(tensor, context, rank):
+    """Key of a prefit basis: the same storage view, unmodified (version counter), same context and rank."""
+    return (tensor.untyped_storage().data_ptr(), tensor.storage_offset(), tuple(tensor.shape), tuple(tensor.stride()),
+            tensor.dtype, str(tensor.device), tensor._version, context, rank)
+
+
+def _prefit_bytes(rows, channels):
+    """(bytes of the largest staged source, bytes per batched matrix: Gram, vectors and workspace)."""
+    return 8 * rows * channels, 12 * channels * channels
+
+
+def _fit_bytes(rows, channels, rank):
+    """Logical workspace of one per-matrix fit (source, Gram, coefficients; FP64-sized with copies)."""
+    return 32 * (rows * channels + channels * channels + rows * rank)
+
+
+# Metrics every fresh-basis GPU fit reports about basis reuse (the GPU path never reuses).
+_NO_REUSE = {"reuse_attempts": 0, "reuse_accepted": False, "reuse_rejections": 0, "reuse_reason": "gpu_fresh_basis",
+             "reuse_seconds": 0.0}
+
+
 class GPUFitter:
-    """Owner-thread GPU fitting facade (``method="gram_batched"``: batched prefit + per-matrix fit)."""
+    """Owner-thread GPU fitting facade (``method="gram_batched"``: batched prefit + per-matrix fit).
+
+    ``shared=True`` lets worker threads call :meth:`fit`: calls serialize on a lock and run on
+    the fitter's private stream (default priority), never on the caller's forward stream.
+    """
 
     def __init__(self, *, gpu_id, gpu_uuid, method="randomized", max_workspace_bytes=2 * 1024**3, seed=0,
                  power_iterations=2, batch_size=60, side_stream=False, shared=False, eigh_solver="auto"):
-        if type(gpu_id) is not int or gpu_id < 0 or not isinstance(gpu_uuid, str) or not gpu_uuid.startswith("GPU-"):
-            raise ConfigurationError("GPU fitting requires an explicit visible device index and UUID")
-        if method not in GPU_FIT_METHODS:
-            raise ConfigurationError("unsupported GPU fitting backend")
-        if type(max_workspace_bytes) is not int or max_workspace_bytes <= 0:
-            raise ConfigurationError("GPU fitting workspace budget must be positive")
-        if type(seed) is not int or seed < 0 or type(power_iterations) is not int or not 0 <= power_iterations <= 8:
-            raise ConfigurationError("invalid GPU fitting seed or iteration count")
-        if type(batch_size) is not int or not 1 <= batch_size <= 256:
-            raise ConfigurationError("GPU fitting batch size must be an integer in [1, 256]")
-        if type(side_stream) is not bool:
-            raise ConfigurationError("side_stream must be boolean")
-        if type(shared) is not bool:
-            raise ConfigurationError("shared must be boolean")
-        if eigh_solver not in EIGH_SOLVERS:
-            raise ConfigurationError(f"eigh_solver must be one of {EIGH_SOLVERS}")
-        self.gpu_id, self.gpu_uuid, self.method = gpu_id, gpu_uuid, method
-        self.max_workspace_bytes, self.seed, self.power_iterations = max_workspace_bytes, seed, power_iterations
-        self.batch_size = batch_size
-        self.eigh_solver = eigh_solver
-        # ``shared`` lets worker threads call ``fit``: calls serialize on a lock and run on the
-        # fitter's private stream (default priority), never on the caller's forward stream.
-        self.shared = shared
-        self.side_stream = side_stream or shared
+        for holds, message in _fitter_rules(gpu_id, gpu_uuid, method, max_workspace_bytes, seed, power_iterations,
+                                            batch_size, side_stream, shared, eigh_solver):
+            need(holds, message)
+        self.gpu_id, self.gpu_uuid, self.method, self.eigh_solver = gpu_id, gpu_uuid, method, eigh_solver
+        self.max_workspace_bytes, self.batch_size = max_workspace_bytes, batch_size
+        self.seed, self.power_iterations = seed, power_iterations
+        self.shared, self.side_stream = shared, side_stream or shared
         self._stream = None
         self._lock = threading.Lock()
         self.owner = (os.getpid(), threading.get_ident())
         self._prefit: dict = {}
         self.prefit_stats = {"batches": 0, "matrices": 0, "hits": 0, "misses": 0, "solver": None}
+
+    # -- ownership and device -------------------------------------------------
 
     def adopt_current_thread(self):
         """Move ownership to the calling thread (not while fitting)."""
@@ -297,38 +336,40 @@ class GPUFitter:
         self.owner = (os.getpid(), threading.get_ident())
 
     def _check_owner(self):
-        if self.shared:
-            if self.owner[0] != os.getpid():
-                raise StateError("a shared GPU fitter cannot cross processes")
-            return
-        if self.owner != (os.getpid(), threading.get_ident()):
-            raise StateError("GPU fitting must run on its configured owner thread, not the CPU encoder pool")
+        pid, thread = self.owner
+        need(pid == os.getpid(), "a shared GPU fitter cannot cross processes" if self.shared else
+             "GPU fitting must run on its configured owner thread, not the CPU encoder pool", StateError)
+        need(self.shared or thread == threading.get_ident(),
+             "GPU fitting must run on its configured owner thread, not the CPU encoder pool", StateError)
 
     def _device(self):
-        if self.gpu_id >= torch.cuda.device_count():
-            raise UnsupportedError("GPU fitting device is unavailable")
+        """The granted device, checked against the UUID the fitter was configured with."""
+        need(self.gpu_id < torch.cuda.device_count(), "GPU fitting device is unavailable", UnsupportedError)
         device = torch.device("cuda", self.gpu_id)
-        actual = str(torch.cuda.get_device_properties(device).uuid)
-        if actual.startswith("GPU-"):
-            actual = actual[len("GPU-"):]
-        if actual != self.gpu_uuid[len("GPU-"):]:
-            raise ConfigurationError("GPU fitting device differs from the granted UUID")
+        actual = str(torch.cuda.get_device_properties(device).uuid).removeprefix("GPU-")
+        need(actual == self.gpu_uuid.removeprefix("GPU-"), "GPU fitting device differs from the granted UUID")
         return device
 
-    def _check_method(self):
-        if self.method not in SUPPORTED_FIT_METHODS:
-            raise UnsupportedError(f"GPU fitting method {self.method!r} is a CUDA library SVD backend; this MI355X "
-                                   f"build fits with {SUPPORTED_FIT_METHODS}")
-
     def _scope(self, device):
-        if self.side_stream and self._stream is None:
+        """The fitter's private stream when it has one, else the caller's current stream."""
+        if not self.side_stream:
+            return contextlib.nullcontext()
+        if self._stream is None:
             self._stream = torch.cuda.Stream(device)
-        return torch.cuda.stream(self._stream) if self.side_stream else contextlib.nullcontext()
+        return torch.cuda.stream(self._stream)
 
-    @staticmethod
-    def _identity(tensor, context, rank):
-        return (tensor.untyped_storage().data_ptr(), tensor.storage_offset(), tuple(tensor.shape), tuple(tensor.stride()),
-                tensor.dtype, str(tensor.device), tensor._version, context, rank)
+    _identity = staticmethod(_tensor_identity)
+
+    # -- batched prefit -------------------------------------------------------
+
+    def _prefit_batch(self, prepared):
+        """Matrices per eigh batch under the workspace budget (at least one, at most ``batch_size``)."""
+        staged, per_matrix = _prefit_bytes(max(int(t.shape[0]) for t, _, _ in prepared),
+                                           max(int(t.shape[1]) for t, _, _ in prepared))
+        spare = self.max_workspace_bytes - staged
+        if spare < per_matrix:
+            raise CapacityError("GPU batched fitting exceeds its declared logical workspace budget")
+        return min(self.batch_size, spare // per_matrix)
 
     @torch.no_grad()
     def prefit(self, items):
@@ -342,117 +383,106 @@ class GPUFitter:
         self.clear_prefit()
         if self.method != "gram_batched" or not items:
             return
-        prepared = []
-        for tensor, context, rank in items.values():
+        prepared = list(items.values())
+        for tensor, context, rank in prepared:
             validate_matrix(tensor, context, lossy=True, check_values=False)
             validate_rank(rank, tuple(tensor.shape))
-            prepared.append((tensor, context, rank))
-        channels = max(int(t.shape[1]) for t, _, _ in prepared)
-        rows = max(int(t.shape[0]) for t, _, _ in prepared)
-        per_item = 3 * 4 * channels * channels
-        if 8 * rows * channels + per_item > self.max_workspace_bytes:
-            raise CapacityError("GPU batched fitting exceeds its declared logical workspace budget")
-        batch = min(self.batch_size, max(1, (self.max_workspace_bytes - 8 * rows * channels) // per_item))
+        batch = self._prefit_batch(prepared)
         device = self._device()
         label, solver = select_eigh_solver(self.eigh_solver)
         self.prefit_stats["solver"] = label
         with torch.cuda.device(device):
-            for start in range(0, len(prepared), batch):
-                group = prepared[start:start + batch]
-                began, ended = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                began.record()
-                sources = [validate_matrix(tensor.to(device), context, check_values=False) for tensor, context, _ in group]
-                if not all_finite(sources):
-                    raise ConfigurationError("lossy input must be finite and representable in FP32")
-                bases = _stored_bases(gram_bases(sources, [rank for _, _, rank in group], eigh=solver))
-                ended.record()
-                ended.synchronize()
-                share = began.elapsed_time(ended) / 1e3 / len(group)
-                del sources
-                for (tensor, context, rank), basis in zip(group, bases):
-                    self._prefit[self._identity(tensor, context, rank)] = (tensor, basis, share)
-                self.prefit_stats["batches"] += 1
-                self.prefit_stats["matrices"] += len(group)
+            for first in range(0, len(prepared), batch):
+                self._solve_group(prepared[first:first + batch], device, solver)
+
+    def _solve_group(self, group, device, solver):
+        marks = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        marks[0].record()
+        sources = [validate_matrix(tensor.to(device), context, check_values=False) for tensor, context, _ in group]
+        need(all_finite(sources), "lossy input must be finite and representable in FP32")
+        bases = _stored_bases(gram_bases(sources, [rank for _, _, rank in group], eigh=solver))
+        marks[1].record()
+        marks[1].synchronize()
+        seconds_each = marks[0].elapsed_time(marks[1]) / 1e3 / len(group)
+        for (tensor, context, rank), basis in zip(group, bases):
+            self._prefit[_tensor_identity(tensor, context, rank)] = (tensor, basis, seconds_each)
+        self.prefit_stats["batches"] += 1
+        self.prefit_stats["matrices"] += len(group)
 
     def clear_prefit(self):
         self._prefit.clear()
 
+    # -- per-matrix fit -------------------------------------------------------
+
     @torch.no_grad()
     def fit(self, tensor, context, rank, *, reuse_basis=None, reuse_threshold=None):
         self._check_owner()
-        if self.shared:
-            with self._lock:
-                return self._fit(tensor, context, rank, reuse_basis=reuse_basis, reuse_threshold=reuse_threshold)
-        return self._fit(tensor, context, rank, reuse_basis=reuse_basis, reuse_threshold=reuse_threshold)
+        with self._lock if self.shared else contextlib.nullcontext():
+            return self._fit(tensor, context, rank, reuse_basis=reuse_basis, reuse_threshold=reuse_threshold)
 
     def _fit(self, tensor, context, rank, *, reuse_basis=None, reuse_threshold=None):
         validate_matrix(tensor, context, lossy=True, check_values=False)
         validate_rank(rank, tuple(tensor.shape))
-        rows, channels = tensor.shape
-        estimated = 32 * (rows * channels + channels * channels + rows * rank)
-        if estimated > self.max_workspace_bytes:
-            raise CapacityError("GPU fitting exceeds its declared logical workspace budget")
+        estimate = _fit_bytes(*tensor.shape, rank)
+        need(estimate <= self.max_workspace_bytes, "GPU fitting exceeds its declared logical workspace budget",
+             CapacityError)
         device = self._device()
-        if reuse_basis is not None or reuse_threshold is not None:
-            raise UnsupportedError("explicit GPU solver comparisons currently require fresh bases")
-        self._check_method()
+        need(reuse_basis is None and reuse_threshold is None,
+             "explicit GPU solver comparisons currently require fresh bases", UnsupportedError)
+        need(self.method in SUPPORTED_FIT_METHODS, f"GPU fitting method {self.method!r} is a CUDA library SVD "
+             f"backend; this MI355X build fits with {SUPPORTED_FIT_METHODS}", UnsupportedError)
         started = time.perf_counter()
-        events = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        # Marks after: nothing, the upload, the fit, the download.
+        marks = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
         with torch.cuda.device(device), self._scope(device):
-            events[0].record()
+            marks[0].record()
             source = tensor.to(device)
-            events[1].record()
+            marks[1].record()
             factors = self._fit_gram_batched(source, tensor, context, rank)
-            events[2].record()
-            basis = factors.basis.cpu()
-            coefficients = factors.coefficients.cpu()
-            events[3].record()
-            events[3].synchronize()
-        metrics = {
-            **factors.metrics, "gpu_fitting_backend": self.method, "gpu_fitting_uuid": self.gpu_uuid,
-            "gpu_fitting_workspace_estimate": estimated,
-            "gpu_fitting_h2d_ms": events[0].elapsed_time(events[1]),
-            "gpu_fitting_compute_ms": events[1].elapsed_time(events[2]),
-            "gpu_fitting_d2h_ms": events[2].elapsed_time(events[3]),
-            "gpu_fitting_wall_seconds": time.perf_counter() - started,
-            "reuse_attempts": 0, "reuse_accepted": False, "reuse_rejections": 0,
-            "reuse_reason": "gpu_fresh_basis", "reuse_seconds": 0.0,
-            "total_factorization_seconds": time.perf_counter() - started,
-            "canonical_basis_rank": rank, "view_rank": rank,
-        }
+            marks[2].record()
+            basis, coefficients = factors.basis.cpu(), factors.coefficients.cpu()
+            marks[3].record()
+            marks[3].synchronize()
+        h2d, compute, d2h = (marks[i].elapsed_time(marks[i + 1]) for i in range(3))
+        wall = time.perf_counter() - started
+        metrics = dict(factors.metrics)
+        metrics.update(gpu_fitting_backend=self.method, gpu_fitting_uuid=self.gpu_uuid,
+                       gpu_fitting_workspace_estimate=estimate, gpu_fitting_h2d_ms=h2d,
+                       gpu_fitting_compute_ms=compute, gpu_fitting_d2h_ms=d2h, gpu_fitting_wall_seconds=wall,
+                       **_NO_REUSE, total_factorization_seconds=wall, canonical_basis_rank=rank, view_rank=rank)
         return Factors(basis=basis, coefficients=coefficients, rank=rank, metrics=metrics)
 
-    def _fit_gram_batched(self, source, tensor, context, rank):
-        """The prefit basis when available; otherwise a single-matrix Gram eigh."""
-        started = time.perf_counter()
-        cached = self._prefit.pop(self._identity(tensor, context, rank), None) if self.method == "gram_batched" else None
+    def _basis_for(self, source, tensor, context, rank):
+        """(stored basis, decomposition seconds, algorithm label, from the prefit cache)."""
+        batched = self.method == "gram_batched"
+        cached = self._prefit.pop(_tensor_identity(tensor, context, rank), None) if batched else None
         if cached is not None:
             validate_matrix(source, context)
             self.prefit_stats["hits"] += 1
-            basis, decomposition_seconds = cached[1], cached[2]
-            algorithm = "batched_fp32_gram_eigh"
-        else:
-            if self.method == "gram_batched":
-                self.prefit_stats["misses"] += 1
-            decomposition_started = time.perf_counter()
-            (basis,) = gram_bases([validate_matrix(source, context)], [rank])
-            (basis,) = _stored_bases([basis])
-            decomposition_seconds = time.perf_counter() - decomposition_started
-            algorithm = "fp32_gram_eigh" if self.method == "gram_batched" else "custom_fp32_gram_eigh"
+            return cached[1], cached[2], "batched_fp32_gram_eigh", True
+        if batched:
+            self.prefit_stats["misses"] += 1
+        clock = time.perf_counter()
+        (basis,) = _stored_bases(gram_bases([validate_matrix(source, context)], [rank]))
+        return basis, time.perf_counter() - clock, "fp32_gram_eigh" if batched else "custom_fp32_gram_eigh", False
+
+    def _fit_gram_batched(self, source, tensor, context, rank):
+        """The prefit basis when available; otherwise a single-matrix Gram eigh; then the projection."""
+        started = time.perf_counter()
+        basis, decomposition, algorithm, prefit = self._basis_for(source, tensor, context, rank)
         projection = project_onto_basis(source, basis, rank=rank, _condition_bound=fast_condition_bound(basis))
-        return Factors(basis=basis, coefficients=projection.coefficients, rank=rank, metrics={
-            "factorization_method": algorithm, "factorization_seed": self.seed,
-            "sketch_rank": None, "power_iterations": 0, "decomposition_count": 1,
-            "svd_count": 0, "eigh_count": 1, "qr_count": 0,
-            "decomposition_seconds": decomposition_seconds,
-            "projection_count": 1, "projection_seconds": projection.seconds,
+        metrics = {
+            "factorization_method": algorithm, "factorization_seed": self.seed, "sketch_rank": None,
+            "power_iterations": 0, "decomposition_count": 1, "svd_count": 0, "eigh_count": 1, "qr_count": 0,
+            "decomposition_seconds": decomposition, "projection_count": 1, "projection_seconds": projection.seconds,
             "projection_relative_residual": projection.relative_residual,
-            "basis_condition_bound": projection.condition_bound,
-            "basis_condition_method": "fp32_neumann_upper_bound",
-            "zero_input": projection.zero_input,
-            "fit_seconds": time.perf_counter() - started,
-            "prefit_batched": cached is not None,
-        })
+            "basis_condition_bound": projection.condition_bound, "basis_condition_method": "fp32_neumann_upper_bound",
+            "zero_input": projection.zero_input, "prefit_batched": prefit,
+        }
+        metrics["fit_seconds"] = time.perf_counter() - started
+        return Factors(basis=basis, coefficients=projection.coefficients, rank=rank, metrics=metrics)
+
+    # -- chunk planning -------------------------------------------------------
 
     @torch.no_grad()
     def plan_chunk(self, config, view, sources, contexts, bindings, parent_rows, *, chunk_id, source_ids,
@@ -460,13 +490,14 @@ class GPUFitter:
         """Energy-target chunk plan on this fitter's device and owner thread (see
         :class:`reelcache_amd.rank_method.GramPlanner`)."""
         from .rank_method import GramPlanner
+
         self._check_owner()
         device = self._device()
         label, solver = select_eigh_solver(self.eigh_solver)
         planner = GramPlanner(config, view, device=device, eigh=solver, eigh_label=label,
                               orthogonalizer=orthogonalizer, max_working_bytes=max_working_bytes)
-        scope = self._lock if self.shared else contextlib.nullcontext()
-        with scope, torch.cuda.device(device), self._scope(device):
+        with self._lock if self.shared else contextlib.nullcontext(), torch.cuda.device(device), \
+                self._scope(device):
             plan = planner.plan(sources, contexts, bindings, parent_rows, chunk_id=chunk_id, source_ids=source_ids)
         self.prefit_stats["solver"] = label
         return plan

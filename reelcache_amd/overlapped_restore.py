@@ -1,12 +1,12 @@
 """Layer-overlapped restore: a history's KV layers are restored on a private stream while the
 model's forward reads the layers already written.
 
-Mirrors the consumer/producer contract of ``reelcache/overlapped_restore.py:70-316``:
+Consumer/producer contract of ``reelcache/overlapped_restore.py:70-316`` (class and method
+names, sources, typed failures, report keys):
 
 * a :class:`LayerReadiness` per restore, with one or more named producers ("sources", e.g. the
   compressed restore and a RAW install); each producer calls :meth:`LayerReadiness.mark` after
-  it has *issued* a layer's writes on its stream (an event is recorded there) and
-  :meth:`LayerReadiness.fail` on an error;
+  it has *issued* a layer's writes on its stream and :meth:`LayerReadiness.fail` on an error;
 * the consumer (the attention of layer ``L``) calls :meth:`LayerReadiness.wait` before reading
   the layer: a host wait until every source issued it, then a device-side wait of the consumer's
   stream on each source's event, so the device never reads a layer before its writes complete
@@ -14,6 +14,12 @@ Mirrors the consumer/producer contract of ``reelcache/overlapped_restore.py:70-3
 * a failure reaches every later ``wait`` and :meth:`LayerReadiness.join` with its class kept for
   this package's errors (``StateError`` otherwise), and stops the other producers at their next
   layer; :meth:`LayerReadiness.cancel` and :meth:`LayerReadiness.quiesce` stop and drain.
+
+Design: the readiness is one state machine under one condition variable.  Each layer holds a
+bit mask of the sources that have not marked it yet and one HIP event per source (recorded at
+the mark on the producer's stream); the run state is ``running`` -> ``stopping`` (cancelled)
+or ``failed``.  Host waits are ``Condition.wait_for`` on "this layer's mask is empty, or the
+run failed"; producers are :class:`_Producer` threads that check the state before each layer.
 
 :func:`start_overlapped_restore` is the compressed-restore producer for this package's hot
 path: it takes the per-layer ``ReconstructionJob`` lists (e.g. from
@@ -32,10 +38,17 @@ from typing import Any, Callable, Sequence
 
 import torch
 
+from ._checks import need
 from .errors import ConfigurationError, ReelCacheError, StateError
 
 #: Source names of the compressed restore and of the RAW install (reference constants).
 RESTORE, RAW = "restore", "raw"
+
+_RUNNING, _STOPPING, _FAILED = "running", "stopping", "failed"
+
+
+def _since(origin, stamps):
+    return [None if stamp is None else stamp - origin for stamp in stamps]
 
 
 class LayerReadiness:
@@ -47,42 +60,36 @@ class LayerReadiness:
 
     def __init__(self, layers: int, device: Any = None, *, timeout: float = 600.0,
                  sources: Sequence[str] = (RESTORE,)) -> None:
-        if type(layers) is not int or layers < 1:
-            raise ConfigurationError("layer readiness needs a positive layer count")
-        if not timeout > 0:
-            raise ConfigurationError("the layer wait timeout must be positive")
         names = tuple(sources)
-        if not names or len(set(names)) != len(names) or any(not isinstance(n, str) or not n for n in names):
-            raise ConfigurationError("readiness sources must be distinct non-empty names")
-        self.layers = layers
-        self.sources = names
-        self.device = torch.device(device) if device is not None else torch.device("cpu")
-        self.timeout = float(timeout)
-        on_gpu = self.device.type == "cuda"
-        self._lock = threading.Lock()
-        self._released = [threading.Event() for _ in range(layers)]
-        self._missing = [set(names) for _ in range(layers)]
-        self._events = [{n: (torch.cuda.Event() if on_gpu else None) for n in names} for _ in range(layers)]
+        need(type(layers) is int and layers >= 1, "layer readiness needs a positive layer count")
+        need(timeout > 0, "the layer wait timeout must be positive")
+        need(names and len(set(names)) == len(names) and all(isinstance(n, str) and n for n in names),
+             "readiness sources must be distinct non-empty names")
+        self.layers, self.sources, self.timeout = layers, names, float(timeout)
+        self.device = torch.device("cpu") if device is None else torch.device(device)
+        self._bit = {name: 1 << index for index, name in enumerate(names)}
+        self._cond = threading.Condition()
+        self._state = _RUNNING
+        self._cancelled = False
         self._error: BaseException | None = None
-        self._stop = threading.Event()
-        self._cancelled = threading.Event()
+        self._unmarked = [(1 << len(names)) - 1] * layers
+        gpu = self.device.type == "cuda"
+        self._events = [[torch.cuda.Event() if gpu else None for _ in names] for _ in range(layers)]
         self._threads: dict[str, threading.Thread] = {}
         self._finished: dict[str, float] = {}
         self.streams: dict[str, Any] = {}
         self.stream = None
         self.created_at = self.called_at = time.perf_counter()
         self.marked_at: list[float | None] = [None] * layers
-        self.source_marked_at = {n: [None] * layers for n in names}
+        self.source_marked_at = {name: [None] * layers for name in names}
         self.waited_seconds = [0.0] * layers
         self.info: dict[str, Any] = {}
 
     def _name(self, source: str | None) -> str:
         if source is None:
-            if len(self.sources) != 1:
-                raise ConfigurationError(f"name the source of a readiness with sources {self.sources}")
+            need(len(self.sources) == 1, f"name the source of a readiness with sources {self.sources}")
             return self.sources[0]
-        if source not in self.sources:
-            raise ConfigurationError(f"unknown readiness source {source!r} (sources {self.sources})")
+        need(source in self._bit, f"unknown readiness source {source!r} (sources {self.sources})")
         return source
 
     # -- producers ------------------------------------------------------------------------------
@@ -91,29 +98,27 @@ class LayerReadiness:
         stream); the layer is released once every source has marked it.  Ignored after a
         failure or a repeated mark."""
         name = self._name(source)
-        with self._lock:
-            if self._error is not None or name not in self._missing[layer]:
+        bit = self._bit[name]
+        with self._cond:
+            if self._state == _FAILED or not self._unmarked[layer] & bit:
                 return
-            event = self._events[layer][name]
+            event = self._events[layer][self.sources.index(name)]
             if event is not None:
-                event.record(stream if stream is not None else torch.cuda.current_stream(self.device))
-            now = time.perf_counter()
-            self._missing[layer].discard(name)
-            self.source_marked_at[name][layer] = now
-            released = not self._missing[layer]
-            if released:
-                self.marked_at[layer] = now
-        if released:
-            self._released[layer].set()
+                event.record(torch.cuda.current_stream(self.device) if stream is None else stream)
+            stamp = time.perf_counter()
+            self.source_marked_at[name][layer] = stamp
+            self._unmarked[layer] &= ~bit
+            if not self._unmarked[layer]:
+                self.marked_at[layer] = stamp
+                self._cond.notify_all()
 
     def fail(self, error: BaseException) -> None:
         """A source failed: every later wait and :meth:`join` raise it; the producers stop."""
-        with self._lock:
+        with self._cond:
             if self._error is None:
                 self._error = error
-        self._stop.set()
-        for flag in self._released:
-            flag.set()
+            self._state = _FAILED
+            self._cond.notify_all()
 
     def attach(self, thread: threading.Thread, source: str | None = None) -> None:
         self._threads[self._name(source)] = thread
@@ -122,12 +127,12 @@ class LayerReadiness:
         """Whether layer ``layer`` is released (``source`` None) or ``source`` has marked it."""
         if source is None:
             return self.marked_at[layer] is not None
-        return self._name(source) not in self._missing[layer]
+        return not self._unmarked[layer] & self._bit[self._name(source)]
 
     @property
     def stopping(self) -> bool:
         """Cancelled or failed: producers stop at their next layer."""
-        return self._stop.is_set()
+        return self._state != _RUNNING
 
     # -- consumer -------------------------------------------------------------------------------
     def wait(self, layer: int, stream: Any = None) -> None:
@@ -135,26 +140,25 @@ class LayerReadiness:
         order ``stream`` (None: the current stream) after every source's writes.  Raises the
         failure (typed) or ``StateError`` after ``timeout`` seconds."""
         begin = time.perf_counter()
-        if not self._released[layer].wait(self.timeout):
+        with self._cond:
+            released = self._cond.wait_for(lambda: self._state == _FAILED or not self._unmarked[layer], self.timeout)
+        if not released:
             raise StateError(f"layer {layer} of the overlapped restore was not issued within {self.timeout} s")
         self.waited_seconds[layer] += time.perf_counter() - begin
         if self._error is not None:
             raise self._failure() from self._error
-        consumer = None
-        for event in self._events[layer].values():
-            if event is None:
-                continue
-            if consumer is None:
-                consumer = stream if stream is not None else torch.cuda.current_stream(self.device)
-            consumer.wait_event(event)
+        events = [event for event in self._events[layer] if event is not None]
+        if events:
+            consumer = torch.cuda.current_stream(self.device) if stream is None else stream
+            for event in events:
+                consumer.wait_event(event)
 
     def ready(self, layer: int) -> bool:
-        return self._released[layer].is_set() and self._error is None
+        return not self._unmarked[layer] and self._error is None
 
     def layer(self, layer: int) -> "LayerWait":
         """Per-layer view (``wait()`` / ``ready()``) for the attention cache of ``layer``."""
-        if type(layer) is not int or not 0 <= layer < self.layers:
-            raise ConfigurationError(f"layer must be an integer in [0, {self.layers})")
+        need(type(layer) is int and 0 <= layer < self.layers, f"layer must be an integer in [0, {self.layers})")
         return LayerWait(self, layer)
 
     @property
@@ -163,73 +167,73 @@ class LayerReadiness:
 
     @property
     def cancelled(self) -> bool:
-        return self._cancelled.is_set()
+        return self._cancelled
 
     @property
     def done(self) -> bool:
         """Every source's producer thread has finished (successfully, failed or cancelled)."""
-        threads = list(self._threads.values())
-        return len(threads) == len(self.sources) and not any(t.is_alive() for t in threads)
+        return set(self._threads) == set(self.sources) and all(not t.is_alive() for t in self._threads.values())
 
     def cancel(self) -> None:
         """Stop every producer at its next layer; no later layer is released."""
-        self._cancelled.set()
-        self._stop.set()
+        with self._cond:
+            self._cancelled = True
+            if self._state == _RUNNING:
+                self._state = _STOPPING
 
-    def _join_threads(self, timeout: float | None, message: str) -> None:
+    def _drain(self, timeout: float | None, message: str) -> None:
+        """Join every producer thread within one deadline; ``StateError(message)`` past it."""
         deadline = time.perf_counter() + (self.timeout if timeout is None else timeout)
         for thread in list(self._threads.values()):
             thread.join(max(0.0, deadline - time.perf_counter()))
-            if thread.is_alive():
-                raise StateError(message)
+            need(not thread.is_alive(), message, StateError)
 
     def quiesce(self, timeout: float | None = None) -> bool:
         """Leave no restore work in flight: cancel unless finished, join the producers, and
         synchronize their streams.  Never raises the restore's failure; True when it completed."""
         if not self.done:
             self.cancel()
-        self._join_threads(timeout, "the overlapped restore did not quiesce")
-        streams = [s for s in self.streams.values() if s is not None]
-        if self.stream is not None and all(s is not self.stream for s in streams):
-            streams.append(self.stream)
-        for stream in streams:
+        self._drain(timeout, "the overlapped restore did not quiesce")
+        streams = {id(s): s for s in (*self.streams.values(), self.stream) if s is not None}
+        for stream in streams.values():
             stream.synchronize()
         return self._error is None
 
     def join(self, timeout: float | None = None) -> dict[str, Any]:
         """Wait for every producer; raise a failure (typed); return the report."""
-        self._join_threads(timeout, "the overlapped restore did not finish")
+        self._drain(timeout, "the overlapped restore did not finish")
         if self._error is not None:
             raise self._failure() from self._error
         return dict(self.info)
 
     def _failure(self) -> ReelCacheError:
+        """The failure re-raised to the consumer: the package error's own class, else StateError."""
         error = self._error
         message = f"overlapped restore failed: {type(error).__name__}: {error}"
-        if isinstance(error, ReelCacheError):
-            with contextlib.suppress(Exception):
-                return type(error)(message)
-        return StateError(message)
+        kind = type(error) if isinstance(error, ReelCacheError) else StateError
+        try:
+            return kind(message)
+        except Exception:  # noqa: BLE001 - an error class with another constructor
+            return StateError(message)
 
     def _finish(self, source: str) -> None:
-        with self._lock:
+        with self._cond:
             self._finished[source] = time.perf_counter()
-            last = len(self._finished) == len(self.sources)
-        if last and self._error is None:
-            marks = [t for t in self.marked_at if t is not None]
-            self.info.update({
-                "overlapped": True, "sources": list(self.sources),
-                "first_layer_ready_seconds_from_call": (min(marks) - self.called_at) if marks else None,
-                "last_layer_ready_seconds_from_call": (max(marks) - self.called_at) if marks else None,
-                "restore_complete_seconds_from_call": max(self._finished.values()) - self.called_at})
+            complete = len(self._finished) == len(self.sources) and self._error is None
+        if not complete:
+            return
+        marks = [stamp - self.called_at for stamp in self.marked_at if stamp is not None]
+        self.info.update(overlapped=True, sources=list(self.sources),
+                         first_layer_ready_seconds_from_call=min(marks) if marks else None,
+                         last_layer_ready_seconds_from_call=max(marks) if marks else None,
+                         restore_complete_seconds_from_call=max(self._finished.values()) - self.called_at)
 
     def timeline(self) -> dict[str, Any]:
         """Marks (seconds after creation) and the consumer's host waits, per layer."""
-        record = {"marked_at": [None if t is None else t - self.created_at for t in self.marked_at],
-                  "waited_seconds": list(self.waited_seconds)}
+        record = {"marked_at": _since(self.created_at, self.marked_at), "waited_seconds": list(self.waited_seconds)}
         if len(self.sources) > 1:
-            record["sources"] = {n: [None if t is None else t - self.created_at for t in marks]
-                                 for n, marks in self.source_marked_at.items()}
+            record["sources"] = {name: _since(self.created_at, stamps)
+                                 for name, stamps in self.source_marked_at.items()}
         return record
 
 
@@ -247,49 +251,68 @@ class LayerWait:
         return self.readiness.ready(self.index)
 
 
-def _producer(readiness: LayerReadiness, source: str, layers: Sequence[int], issue: Callable[[int, Any], Any],
-              stream: Any, wait_event: Any) -> None:
-    """Issue layers in order on ``stream`` (None on the CPU), marking each; stop when asked."""
-    grad = torch.is_grad_enabled()
-    inference = torch.is_inference_mode_enabled()
+class _Producer(threading.Thread):
+    """Issues one source's layers in order on its stream (None on the CPU), marking each; stops
+    when the readiness is stopping; reports any error to the readiness.  The caller's grad and
+    inference modes carry over to the thread."""
 
-    def run() -> None:
+    def __init__(self, readiness, source, layers, issue, stream, wait_event):
+        super().__init__(name=f"reelcache-overlapped-{source}", daemon=True)
+        self.readiness, self.source, self.layers, self.issue = readiness, source, layers, issue
+        self.stream, self.wait_event = stream, wait_event
+        self.modes = (torch.is_inference_mode_enabled(), torch.is_grad_enabled())
+
+    def _issue_all(self):
+        readiness, stream = self.readiness, self.stream
+        if stream is not None and self.wait_event is not None:
+            stream.wait_event(self.wait_event)
+        results = []
+        for layer in self.layers:
+            if readiness.stopping:
+                raise StateError("overlapped restore cancelled" if readiness.cancelled
+                                 else "another source of the overlapped restore failed")
+            results.append(self.issue(layer, stream))
+            readiness.mark(layer, stream, self.source)
+        if stream is not None:
+            stream.synchronize()  # every layer's work completed before the producer reports done
+        for result in results:
+            getattr(result, "release", lambda: None)()
+
+    def run(self):
+        inference, grad = self.modes
         try:
             with torch.inference_mode(inference), torch.set_grad_enabled(grad), \
-                    (torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext()):
-                if wait_event is not None and stream is not None:
-                    stream.wait_event(wait_event)
-                keep = []
-                for layer in layers:
-                    if readiness.stopping:
-                        raise StateError("overlapped restore cancelled" if readiness.cancelled
-                                         else "another source of the overlapped restore failed")
-                    keep.append(issue(layer, stream))
-                    readiness.mark(layer, stream, source)
-                if stream is not None:
-                    stream.synchronize()  # every layer's work completed before the producer reports done
-                for item in keep:
-                    release = getattr(item, "release", None)
-                    if release is not None:
-                        release()
+                    (torch.cuda.stream(self.stream) if self.stream is not None else contextlib.nullcontext()):
+                self._issue_all()
         except BaseException as error:  # noqa: BLE001 - delivered to the consumer, typed
-            readiness.fail(error)
+            self.readiness.fail(error)
         finally:
-            readiness._finish(source)
+            self.readiness._finish(self.source)
 
-    thread = threading.Thread(target=run, name=f"reelcache-overlapped-{source}", daemon=True)
+
+def _producer(readiness: LayerReadiness, source: str, layers: Sequence[int], issue: Callable[[int, Any], Any],
+              stream: Any, wait_event: Any) -> None:
+    thread = _Producer(readiness, source, layers, issue, stream, wait_event)
     readiness.attach(thread, source)
     thread.start()
 
 
 def _stream_for(readiness: LayerReadiness, source: str):
+    """A private stream (default priority) for ``source`` on a GPU readiness; None on the CPU."""
     if readiness.device.type != "cuda":
         return None
-    stream = torch.cuda.Stream(readiness.device)
-    readiness.streams[source] = stream
+    stream = readiness.streams[source] = torch.cuda.Stream(readiness.device)
     if readiness.stream is None or source == RESTORE:
         readiness.stream = stream
     return stream
+
+
+def _checked(readiness, layers, source, device, timeout):
+    if readiness is None:
+        return LayerReadiness(layers, device, timeout=timeout, sources=(source,))
+    if readiness.layers != layers or source not in readiness.sources:
+        raise ConfigurationError(f"the readiness must cover {layers} layers and have a {source!r} source")
+    return readiness
 
 
 def start_overlapped_restore(layer_jobs: Sequence[Sequence[Any]], *, device: Any = None, precision: str = "auto",
@@ -302,20 +325,13 @@ def start_overlapped_restore(layer_jobs: Sequence[Sequence[Any]], *, device: Any
     history with a RAW install as the other source)."""
     from . import restore_kernels as rk
 
-    layers = len(layer_jobs)
-    if readiness is None:
-        readiness = LayerReadiness(layers, device, timeout=timeout, sources=(RESTORE,))
-    elif readiness.layers != layers or RESTORE not in readiness.sources:
-        raise ConfigurationError("the readiness must cover the restored layers and have a 'restore' source")
-    stream = _stream_for(readiness, RESTORE)
+    readiness = _checked(readiness, len(layer_jobs), RESTORE, device, timeout)
 
     def issue(layer: int, on: Any):
         jobs = list(layer_jobs[layer])
-        if not jobs:
-            return None
-        return rk.reconstruct(jobs, stream=on, precision=precision, config=config)
+        return rk.reconstruct(jobs, stream=on, precision=precision, config=config) if jobs else None
 
-    _producer(readiness, RESTORE, range(layers), issue, stream, wait_event)
+    _producer(readiness, RESTORE, range(len(layer_jobs)), issue, _stream_for(readiness, RESTORE), wait_event)
     return readiness
 
 
@@ -324,10 +340,7 @@ def start_overlapped_install(raw: Callable[[int], Any], *, layers: int, device: 
                              source: str = RAW) -> LayerReadiness:
     """Run ``raw(layer)`` for every layer in order on a private stream (a RAW install: dense
     K / V copied and stored by the caller's function), marking each layer."""
-    if readiness is None:
-        readiness = LayerReadiness(layers, device, timeout=timeout, sources=(source,))
-    elif readiness.layers != layers or source not in readiness.sources:
-        raise ConfigurationError(f"the readiness must cover {layers} layers and have a {source!r} source")
-    stream = _stream_for(readiness, source)
-    _producer(readiness, source, range(layers), lambda layer, on: raw(layer), stream, wait_event)
+    readiness = _checked(readiness, layers, source, device, timeout)
+    _producer(readiness, source, range(layers), lambda layer, on: raw(layer), _stream_for(readiness, source),
+              wait_event)
     return readiness

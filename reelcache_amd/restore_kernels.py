@@ -45,24 +45,26 @@ never changes process-wide torch settings.
 
 from __future__ import annotations
 
+import contextlib
 import math
 import threading
-import time
-from collections.abc import Mapping, Sequence
-from dataclasses import dataclass, field
-from typing import Any
 
 import numpy as np
 import torch
 
 from . import _lib
 from .errors import ConfigurationError, IntegrityError, StateError, UnsupportedError
+from ._checks import need
+from .restore_handle import RestoreHandle, _sweep_deferred, park_failed, pending_deferred
+from .restore_model import (COEFFICIENT_DTYPES, LAYOUTS, OUTPUT_DTYPES, CoefficientSource, DenseSource, NativeView, PictureSource, ReconstructionJob,
+                            RopePositions, RopeTable, expand_affine, wan_sections)
+from .restore_reference import (_OUTPUT_FLOOR, _UNIT_ROUNDOFF, _check_compute_dtype, _check_disjoint, _gemm_gamma,
+                                _native_rotation, _require_fp32_matmul, _storage_key, _validate, apply_rope_reference, dequantize,
+                                error_bound, fp32_matmul_precision, reconstruct_reference, reference_coefficients,
+                                reference_values, rope_cos_sin, unpack_pictures)
 
-LAYOUTS = ("BTHD", "THD", "BHTD")
 PRECISIONS = ("fp32", "tf32", "tf32x3", "fp16", "fp16x2", "bf16")
 BACKENDS = ("auto", "reference", "fused", "two_pass", "staged", "interpret")
-OUTPUT_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
-COEFFICIENT_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
 BASIS_DTYPES = (torch.float16, torch.bfloat16)
 
 #: Why the compiled HIP kernels cannot be used in this process (None when they can).
@@ -86,946 +88,6 @@ _REFERENCE_TILE_KEYS = {"BLOCK_M", "BLOCK_K", "num_warps", "num_stages", "N_GROU
                         "maxnreg", "_n_group"}
 
 
-def _int(value, name, *, minimum=0):
-    if type(value) is not int or value < minimum:
-        raise ConfigurationError(f"{name} must be an integer >= {minimum}")
-    return value
-
-
-def _require_tensor(value, name):
-    if not isinstance(value, torch.Tensor) or value.layout != torch.strided:
-        raise ConfigurationError(f"{name} must be a strided torch.Tensor")
-    if value.device.type == "meta":
-        raise ConfigurationError(f"{name} cannot be a meta tensor")
-    return value
-
-
-def _host_vector(value, length, name):
-    """FP32 host copy of a per-rank-column affine vector."""
-    if isinstance(value, torch.Tensor):
-        if value.device.type != "cpu":
-            raise ConfigurationError(f"{name} must be a host array; pass the packet affine payload")
-        value = value.detach().numpy()
-    array = np.asarray(value)
-    if array.dtype != np.float32 or array.shape != (length,):
-        raise ConfigurationError(f"{name} must be a float32 vector with one entry per rank column")
-    if not np.isfinite(array).all():
-        raise ConfigurationError(f"{name} must be finite")
-    return np.ascontiguousarray(array)
-
-
-def expand_affine(affine, normalization, rank):
-    """Per-column ``(scale, offset)`` from a packet affine payload ``[2, records]``.
-
-    ``per_channel``: one record per column.  ``global`` / ``leading_columns``:
-    record 0 is shared by the unprotected columns and records ``1..count`` belong
-    to the leading ``protected_count`` columns (reelcache/restore_kernels.py:204-227,
-    reelcache/_hevc.py:475-483).
-    """
-    affine = np.asarray(affine)
-    if affine.dtype != np.dtype("<f4") or affine.ndim != 2 or affine.shape[0] != 2:
-        raise ConfigurationError("affine must be a little-endian float32 [2, records] array")
-    if not isinstance(normalization, Mapping) or "mode" not in normalization:
-        raise ConfigurationError("normalization must be the packet normalization layout")
-    _int(rank, "rank", minimum=1)
-    if normalization["mode"] == "per_channel":
-        if affine.shape[1] != rank:
-            raise ConfigurationError("per-channel affine must have one record per rank column")
-        return affine[0].copy(), affine[1].copy()
-    count = normalization["protected_count"]
-    if type(count) is not int or not 0 <= count <= rank or affine.shape[1] != count + 1:
-        raise ConfigurationError("affine record count differs from the protected columns")
-    scale = np.full(rank, affine[0, 0], dtype=np.float32)
-    offset = np.full(rank, affine[1, 0], dtype=np.float32)
-    scale[:count] = affine[0, 1:]
-    offset[:count] = affine[1, 1:]
-    return scale, offset
-
-
-# ---------------------------------------------------------------------------
-# Destinations, RoPE tables and sources
-# ---------------------------------------------------------------------------
-
-
-@dataclass(frozen=True, eq=False)
-class NativeView:
-    """A native cache tensor, its layout and the first destination token.
-
-    ``"BTHD"``: Wan/SGLang ``[B, T, H, D]``; ``"THD"``: RAVEN packed ``[T, H, D]``;
-    ``"BHTD"``: LongCat ``[B, H, T, D]``.  Any strides are accepted.
-    """
-
-    tensor: torch.Tensor
-    layout: str = "BTHD"
-    token_offset: int = 0
-    batch_index: int = 0
-
-    def __post_init__(self):
-        tensor = _require_tensor(self.tensor, "destination tensor")
-        if self.layout not in LAYOUTS:
-            raise ConfigurationError(f"destination layout must be one of {LAYOUTS}")
-        if tensor.ndim != (3 if self.layout == "THD" else 4):
-            raise ConfigurationError(f"{self.layout} destination has the wrong number of dimensions")
-        if tensor.dtype not in OUTPUT_DTYPES:
-            raise ConfigurationError("destination dtype must be bfloat16, float16 or float32")
-        _int(self.token_offset, "token_offset")
-        _int(self.batch_index, "batch_index")
-        if self.layout == "THD" and self.batch_index:
-            raise ConfigurationError("a packed THD destination has no batch dimension")
-        if self.layout != "THD" and self.batch_index >= tensor.shape[0]:
-            raise ConfigurationError("batch_index is outside the destination")
-        if self.head_dim % 2:
-            raise ConfigurationError("head_dim must be even")
-        if any(size > 1 and stride == 0 for size, stride in zip(tensor.shape, tensor.stride())):
-            raise ConfigurationError("destination views with broadcast (zero) strides alias")
-
-    @property
-    def heads(self):
-        return self.tensor.shape[1] if self.layout == "BHTD" else self.tensor.shape[-2]
-
-    @property
-    def head_dim(self):
-        return self.tensor.shape[-1]
-
-    @property
-    def channels(self):
-        return self.heads * self.head_dim
-
-    @property
-    def capacity(self):
-        return self.tensor.shape[2] if self.layout == "BHTD" else self.tensor.shape[-3]
-
-    def strides(self):
-        """Element strides of (token, head, dim)."""
-        stride = self.tensor.stride()
-        if self.layout == "BHTD":
-            return stride[2], stride[1], stride[3]
-        return stride[-3], stride[-2], stride[-1]
-
-    def element_offset(self):
-        """Element offset (in the storage) of (batch_index, token_offset, head 0, dim 0)."""
-        base = self.tensor.storage_offset()
-        if self.layout != "THD":
-            base += self.batch_index * self.tensor.stride(0)
-        return base + self.token_offset * self.strides()[0]
-
-    def slot(self, tokens):
-        """A ``[tokens, H, D]`` view of the destination slot."""
-        stop = self.token_offset + tokens
-        if self.layout == "THD":
-            return self.tensor[self.token_offset:stop]
-        if self.layout == "BTHD":
-            return self.tensor[self.batch_index, self.token_offset:stop]
-        return self.tensor[self.batch_index, :, self.token_offset:stop].transpose(0, 1)
-
-
-def wan_sections(pairs):
-    """Wan/LongCat 3-D split of ``pairs = head_dim // 2`` into (t, h, w) pair counts."""
-    _int(pairs, "pairs", minimum=1)
-    third = pairs // 3
-    return (pairs - 2 * third, third, third)
-
-
-_UPLOAD_STREAMS: dict = {}
-_UPLOAD_LOCK = threading.Lock()
-
-
-def _upload_stream(device):
-    """Private per-device stream for RoPE-table uploads (default priority)."""
-    with _UPLOAD_LOCK:
-        stream = _UPLOAD_STREAMS.get(device)
-        if stream is None:
-            stream = _UPLOAD_STREAMS[device] = torch.cuda.Stream(device)
-        return stream
-
-
-class _KernelTables:
-    """FP32 device copies of one table -- ``cos``, ``sin`` and the interleaved ``pairs``
-    ``[rows, pairs, 2]`` the straight-line kernels read -- and the event that completes all three.
-
-    Every consumer stream waits on the event (``order_before``) until it has completed, so a
-    call on any stream that finds the cached entry cannot read a table before it is written."""
-
-    __slots__ = ("cos", "event", "pairs", "sin", "staging", "stamp")
-
-    def __init__(self, cos, sin, pairs, stamp, event=None, staging=None):
-        self.cos, self.sin, self.pairs, self.stamp, self.event, self.staging = cos, sin, pairs, stamp, event, staging
-
-    @classmethod
-    def make(cls, cos, sin, device, stream, stamp):
-        on_device = device.type == "cuda"
-        with torch.inference_mode(False), torch.no_grad():
-            if not on_device:
-                cos32, sin32 = (t.to(device=device, dtype=torch.float32).contiguous() for t in (cos, sin))
-                return cls(cos32, sin32, torch.stack((cos32, sin32), dim=-1).contiguous(), stamp)
-            if torch.cuda.is_current_stream_capturing():
-                # Work enqueued now would only run when the graph replays, and eager calls
-                # before the first replay would read unwritten tables.
-                raise ConfigurationError("a RoPE table's device copy cannot be built during HIP-graph capture: "
-                                         "run one call with the table (or warmup) before capturing")
-            staging = None
-            if cos.device.type == "cpu":
-                # Read the host tables now into private pinned memory; upload on a private stream.
-                staging = tuple(torch.empty(t.shape, dtype=torch.float32, pin_memory=True).copy_(t) for t in (cos, sin))
-                work = _upload_stream(device)
-            else:
-                work = torch.cuda.current_stream(device) if stream is None else stream
-            with torch.cuda.stream(work):
-                if staging is not None:
-                    cos32, sin32 = (torch.empty(t.shape, dtype=torch.float32, device=device) for t in staging)
-                    cos32.copy_(staging[0], non_blocking=True)
-                    sin32.copy_(staging[1], non_blocking=True)
-                else:
-                    # A contiguous float32 device table is used in place; other dtypes / layouts
-                    # are converted after the work already enqueued on the caller's stream.
-                    cos32, sin32 = (t.to(device=device, dtype=torch.float32).contiguous() for t in (cos, sin))
-                pairs = torch.stack((cos32, sin32), dim=-1).contiguous()
-                event = torch.cuda.Event()
-                event.record(work)
-            return cls(cos32, sin32, pairs, stamp, event, staging)
-
-    def order_before(self, device, stream):
-        """Make ``stream`` (default: current) wait for the copies; no-op once complete."""
-        event = self.event
-        if event is None:
-            return
-        if event.query():
-            self.event = None
-            self.staging = None
-            return
-        (torch.cuda.current_stream(device) if stream is None else stream).wait_event(event)
-
-
-@dataclass(frozen=True, eq=False)
-class RopeTable:
-    """cos/sin rotation tables ``[R, head_dim // 2]`` for interleaved pairs.
-
-    ``sections=(t, h, w)`` makes the table separable: pair ``j`` of a token at
-    (frame f, row y, column x) uses row ``t_row + f`` when ``j < t``, row
-    ``h_row + y`` when ``j < t + h`` and row ``w_row + x`` otherwise.
-    ``sections=None`` is a dense per-token table (row ``row + n`` for token ``n``).
-    Tables are float64 or float32; the GPU kernels use float32 device copies
-    (:meth:`kernel_tables`), the reference backend the table's own precision.
-    """
-
-    cos: torch.Tensor
-    sin: torch.Tensor
-    sections: tuple | None = None
-    section_rows: tuple | None = None
-    _device_cache: dict = field(default_factory=dict, init=False, repr=False, compare=False)
-    _inference: bool = field(default=False, init=False, repr=False, compare=False)
-
-    def __post_init__(self):
-        cos, sin = _require_tensor(self.cos, "RoPE cos"), _require_tensor(self.sin, "RoPE sin")
-        if (cos.ndim != 2 or cos.shape != sin.shape or cos.dtype != sin.dtype
-                or cos.dtype not in (torch.float32, torch.float64) or cos.device != sin.device or min(cos.shape) < 1):
-            raise ConfigurationError("RoPE cos/sin must be matching float32/float64 [rows, head_dim // 2] tensors")
-        object.__setattr__(self, "_inference", cos.is_inference() or sin.is_inference())
-        rows, pairs = cos.shape
-        if self.sections is not None:
-            sections = tuple(self.sections)
-            if len(sections) != 3 or any(type(v) is not int or v < 0 for v in sections) or sum(sections) != pairs:
-                raise ConfigurationError("RoPE sections must be three nonnegative pair counts summing to head_dim // 2")
-            object.__setattr__(self, "sections", sections)
-            limits = (rows, rows, rows) if self.section_rows is None else tuple(self.section_rows)
-            if len(limits) != 3 or any(type(v) is not int or not 0 <= v <= rows for v in limits):
-                raise ConfigurationError("section_rows must be three row counts within the table")
-            object.__setattr__(self, "section_rows", limits)
-        elif self.section_rows is not None:
-            raise ConfigurationError("section_rows requires separable sections")
-
-    @property
-    def rows(self):
-        return self.cos.shape[0]
-
-    @property
-    def pairs(self):
-        return self.cos.shape[1]
-
-    @property
-    def head_dim(self):
-        return 2 * self.pairs
-
-    @classmethod
-    def from_complex(cls, freqs, sections="wan"):
-        """From complex ``freqs[rows, head_dim // 2]`` (the Wan ``rope_params`` concatenation)."""
-        freqs = _require_tensor(freqs, "freqs")
-        if not freqs.is_complex() or freqs.ndim != 2:
-            raise ConfigurationError("freqs must be a complex [rows, head_dim // 2] tensor")
-        real = torch.view_as_real(freqs.resolve_conj())
-        dtype = torch.float64 if freqs.dtype == torch.complex128 else torch.float32
-        if sections == "wan":
-            sections = wan_sections(freqs.shape[1])
-        return cls(real[..., 0].to(dtype).contiguous(), real[..., 1].to(dtype).contiguous(), sections)
-
-    @classmethod
-    def from_axes(cls, temporal, height, width):
-        """Separable table from per-axis complex tensors ``[positions, pairs]`` (unused cells NaN)."""
-        axes = [_require_tensor(value, "axis freqs") for value in (temporal, height, width)]
-        if any(not value.is_complex() or value.ndim != 2 for value in axes):
-            raise ConfigurationError("axis frequencies must be complex [positions, pairs] tensors")
-        if len({value.device for value in axes}) != 1:
-            raise ConfigurationError("axis frequencies must share a device")
-        dtype = torch.float64 if all(value.dtype == torch.complex128 for value in axes) else torch.float32
-        rows = max(value.shape[0] for value in axes)
-        pairs = sum(value.shape[1] for value in axes)
-        cos = torch.full((rows, pairs), float("nan"), dtype=dtype, device=axes[0].device)
-        sin = torch.full_like(cos, float("nan"))
-        column = 0
-        for value in axes:
-            real = torch.view_as_real(value.resolve_conj()).to(dtype)
-            cos[:value.shape[0], column:column + value.shape[1]] = real[..., 0]
-            sin[:value.shape[0], column:column + value.shape[1]] = real[..., 1]
-            column += value.shape[1]
-        return cls(cos, sin, tuple(value.shape[1] for value in axes), tuple(value.shape[0] for value in axes))
-
-    @classmethod
-    def from_cos_sin(cls, cos, sin, sections=None):
-        """From real tables, e.g. SGLang's dense ``freqs_cis = (cos, sin)``."""
-        return cls(cos, sin, sections)
-
-    @classmethod
-    def longcat(cls, head_dim, num_frames, height, width, *, base=10000.0, device="cpu"):
-        """LongCat-Video ``rope_3d`` tables in float32 (angles and cos/sin of float32 angles).
-
-        LongCat's KV cache stores pre-RoPE K, so restored LongCat caches are written
-        without rotation; the table serves the engine's own RoPE.
-        """
-        _int(head_dim, "head_dim", minimum=8)
-        if head_dim % 8:
-            raise ConfigurationError("LongCat 3D RoPE requires head_dim divisible by 8")
-        for value, name in ((num_frames, "num_frames"), (height, "height"), (width, "width")):
-            _int(value, name, minimum=1)
-        sixth = head_dim // 6
-        dims = (head_dim - 4 * sixth, 2 * sixth, 2 * sixth)
-        tables = []
-        for dim, count in zip(dims, (num_frames, height, width)):
-            inverse = 1.0 / (base ** (torch.arange(0, dim, 2)[: dim // 2].float() / dim))
-            grid = torch.from_numpy(np.linspace(0, count, count, endpoint=False, dtype=np.float32)).float()
-            tables.append(grid[:, None] * inverse[None, :])
-        rows = max(table.shape[0] for table in tables)
-        pairs = sum(table.shape[1] for table in tables)
-        cos = torch.full((rows, pairs), float("nan"), dtype=torch.float32)
-        sin = torch.full_like(cos, float("nan"))
-        column = 0
-        for table in tables:
-            cos[:table.shape[0], column:column + table.shape[1]] = table.cos()
-            sin[:table.shape[0], column:column + table.shape[1]] = table.sin()
-            column += table.shape[1]
-        return cls(cos.to(device), sin.to(device), tuple(t.shape[1] for t in tables), tuple(t.shape[0] for t in tables))
-
-    def _stamp(self):
-        if self._inference:
-            return (self.cos.data_ptr(), self.sin.data_ptr())
-        return (self.cos._version, self.sin._version)
-
-    def invalidate(self):
-        """Drop the cached device copies (after updating inference-tensor tables in place)."""
-        self._device_cache.clear()
-
-    def kernel_tables(self, device, stream=None):
-        """Contiguous float32 ``(cos, sin)`` on ``device``, valid for work enqueued next on ``stream``."""
-        device = torch.device(device)
-        if device.type == "cuda" and device.index is None:
-            device = torch.device("cuda", torch.cuda.current_device())
-        stamp = self._stamp()
-        entry = self._device_cache.get(device)
-        if entry is None or entry.stamp != stamp:
-            entry = _KernelTables.make(self.cos, self.sin, device, stream, stamp)
-            self._device_cache[device] = entry
-        if entry.event is not None:
-            entry.order_before(device, stream)
-        return entry.cos, entry.sin
-
-    def kernel_pairs(self, device, stream=None):
-        """Interleaved float32 ``[rows, pairs, 2]`` (cos, sin) on ``device``, valid for work enqueued
-        next on ``stream`` (built with :meth:`kernel_tables`' copies and ordered by the same event)."""
-        cos, _ = self.kernel_tables(device, stream)
-        return self._device_cache[cos.device].pairs
-
-
-@dataclass(frozen=True, eq=False)
-class RopePositions:
-    """Original positions of one chunk in a :class:`RopeTable`.
-
-    Separable tables take ``rows=(t_row, h_row, w_row)`` (an int means
-    ``(t_row, 0, 0)``); dense tables take ``rows=first_row``.
-    """
-
-    table: RopeTable
-    rows: Any = 0
-
-    def __post_init__(self):
-        if not isinstance(self.table, RopeTable):
-            raise ConfigurationError("RoPE positions require a RopeTable")
-        if self.table.sections is None:
-            _int(self.rows, "dense RoPE row")
-            return
-        rows = (self.rows, 0, 0) if type(self.rows) is int else tuple(self.rows)
-        if len(rows) != 3:
-            raise ConfigurationError("separable RoPE positions are (t_row, h_row, w_row)")
-        for value in rows:
-            _int(value, "RoPE row")
-        object.__setattr__(self, "rows", rows)
-
-
-@dataclass(frozen=True, eq=False)
-class CoefficientSource:
-    """Coefficients ``[N, >= rank]`` already unpacked from their pictures.
-
-    Float values are used as is; ``uint8`` values are quantized pixels with the
-    per-column FP32 affine ``scale``/``offset`` as host arrays.  ``bound``
-    optionally bounds ``|values|`` for the FP16 modes' power-of-two prescale.
-    """
-
-    values: torch.Tensor
-    scale: Any = None
-    offset: Any = None
-    bound: float | None = None
-
-    def __post_init__(self):
-        values = _require_tensor(self.values, "coefficients")
-        if values.ndim != 2:
-            raise ConfigurationError("coefficients must be a [tokens, rank] matrix")
-        if self.bound is not None and (isinstance(self.bound, bool) or not isinstance(self.bound, (int, float))
-                                       or not math.isfinite(self.bound) or self.bound < 0):
-            raise ConfigurationError("bound must be a finite nonnegative upper bound on |coefficients|")
-        if values.dtype == torch.uint8:
-            if self.scale is None or self.offset is None:
-                raise ConfigurationError("quantized coefficients require their affine scale and offset")
-            object.__setattr__(self, "scale", _host_vector(self.scale, values.shape[1], "scale"))
-            object.__setattr__(self, "offset", _host_vector(self.offset, values.shape[1], "offset"))
-            if np.any(self.scale < 0):
-                raise ConfigurationError("affine scales must be nonnegative")
-        elif values.dtype in COEFFICIENT_DTYPES:
-            if self.scale is not None or self.offset is not None:
-                raise ConfigurationError("dequantized coefficients take no affine")
-        else:
-            raise ConfigurationError("coefficients must be uint8 pixels or float32/float16/bfloat16 values")
-
-    @property
-    def quantized(self):
-        return self.values.dtype == torch.uint8
-
-
-@dataclass(frozen=True, eq=False)
-class PictureSource:
-    """Quantized coefficients read in place from decoded pictures.
-
-    ``pictures[segment][frame]`` is a uint8 view ``[planes, rows, columns]``
-    whose origin is this matrix's rectangle; all views share plane and row
-    strides and have unit column stride.  ``layout`` is the matrix's
-    ``reelcache.channel_tiles.v1`` layout, ``scale``/``offset`` its expanded affine.
-    """
-
-    pictures: Any
-    layout: Mapping
-    scale: Any
-    offset: Any
-
-    def __post_init__(self):
-        layout = self.layout
-        required = ("frames", "height", "width", "rank", "planes", "grid", "channels_per_segment", "segments")
-        if not isinstance(layout, Mapping) or any(name not in layout for name in required):
-            raise ConfigurationError("picture layout must be a reelcache.channel_tiles.v1 layout")
-        frames, height, width, rank = (layout[name] for name in ("frames", "height", "width", "rank"))
-        planes, slots, segments = layout["planes"], layout["channels_per_segment"], layout["segments"]
-        for value, name in ((frames, "frames"), (height, "height"), (width, "width"), (rank, "rank"),
-                            (planes, "planes"), (slots, "channels_per_segment"), (segments, "segments")):
-            _int(value, f"layout {name}", minimum=1)
-        columns, rows = layout["grid"]
-        _int(columns, "grid columns", minimum=1)
-        _int(rows, "grid rows", minimum=1)
-        if slots != columns * rows * planes or segments != math.ceil(rank / slots):
-            raise ConfigurationError("picture layout slot/segment counts are inconsistent")
-        pictures = tuple(tuple(segment) for segment in self.pictures)
-        if len(pictures) != segments or any(len(segment) != frames for segment in pictures):
-            raise ConfigurationError("pictures must be indexed [segment][frame] for every segment and frame")
-        strides = device = None
-        for segment in pictures:
-            for picture in segment:
-                _require_tensor(picture, "picture")
-                if picture.dtype != torch.uint8 or picture.ndim != 3:
-                    raise ConfigurationError("pictures must be uint8 [planes, rows, columns] views")
-                if picture.shape[0] < planes or picture.shape[1] < rows * height or picture.shape[2] < columns * width:
-                    raise ConfigurationError("picture view does not cover the matrix rectangle")
-                if picture.stride(2) != 1:
-                    raise ConfigurationError("picture rows must be contiguous (unit column stride)")
-                current = (picture.stride(0), picture.stride(1))
-                if strides is None:
-                    strides, device = current, picture.device
-                elif current != strides or picture.device != device:
-                    raise ConfigurationError("pictures of one matrix must share plane/row strides and device")
-        object.__setattr__(self, "pictures", pictures)
-        object.__setattr__(self, "scale", _host_vector(self.scale, rank, "scale"))
-        object.__setattr__(self, "offset", _host_vector(self.offset, rank, "offset"))
-        if np.any(self.scale < 0):
-            raise ConfigurationError("affine scales must be nonnegative")
-
-    @property
-    def device(self):
-        return self.pictures[0][0].device
-
-    @property
-    def rank(self):
-        return self.layout["rank"]
-
-    @property
-    def plane_stride(self):
-        return self.pictures[0][0].stride(0)
-
-    @property
-    def row_stride(self):
-        return self.pictures[0][0].stride(1)
-
-    @classmethod
-    def from_canvases(cls, canvases, layout, picture_indices, origins, scale, offset):
-        """Views on decoded canvases ``[pictures, planes, height, width]``.
-
-        ``picture_indices[segment][frame]`` selects the canvas picture; ``origins`` is
-        one ``(y, x)`` for the matrix or a ``[segment][frame]`` table of origins.
-        """
-        canvases = _require_tensor(canvases, "canvases")
-        if canvases.ndim != 4 or canvases.dtype != torch.uint8:
-            raise ConfigurationError("canvases must be uint8 [pictures, planes, height, width]")
-        single = len(origins) == 2 and all(type(value) is int for value in origins)
-        pictures = []
-        for segment_index, segment in enumerate(picture_indices):
-            row = []
-            for frame_index, picture in enumerate(segment):
-                y, x = origins if single else origins[segment_index][frame_index]
-                _int(picture, "picture index")
-                _int(y, "rectangle y")
-                _int(x, "rectangle x")
-                if picture >= canvases.shape[0]:
-                    raise ConfigurationError("picture index is outside the canvases")
-                row.append(canvases[picture, :, y:, x:])
-            pictures.append(tuple(row))
-        return cls(tuple(pictures), layout, scale, offset)
-
-
-@dataclass(frozen=True, eq=False)
-class DenseSource:
-    """An uncompressed canonical ``[N, C]`` matrix (RAW archive, exact path)."""
-
-    values: torch.Tensor
-
-    def __post_init__(self):
-        values = _require_tensor(self.values, "dense values")
-        if values.ndim != 2 or values.dtype not in COEFFICIENT_DTYPES:
-            raise ConfigurationError("dense values must be a float32/float16/bfloat16 [tokens, channels] matrix")
-
-
-@dataclass(frozen=True, eq=False)
-class ReconstructionJob:
-    """Reconstruct one restored matrix into one native destination slot.
-
-    ``grid=(frames, height, width)`` is the chunk's token geometry.  Factorized
-    sources need ``basis`` (rows ``[R, C]``) and use the prefix view
-    ``basis[:rank]`` (``rank`` defaults to the source's coefficient columns).
-    ``rope=None`` writes without rotation (V, or pre-RoPE K caches such as LongCat's).
-    """
-
-    source: Any
-    destination: NativeView
-    grid: tuple
-    basis: torch.Tensor | None = None
-    rank: int | None = None
-    rope: RopePositions | None = None
-    label: str | None = None
-
-    def __post_init__(self):
-        if not isinstance(self.source, (CoefficientSource, PictureSource, DenseSource)):
-            raise ConfigurationError("source must be a CoefficientSource, PictureSource or DenseSource")
-        if not isinstance(self.destination, NativeView):
-            raise ConfigurationError("destination must be a NativeView")
-        grid = tuple(self.grid)
-        if len(grid) != 3:
-            raise ConfigurationError("grid must be (frames, height, width)")
-        for value in grid:
-            _int(value, "grid size", minimum=1)
-        object.__setattr__(self, "grid", grid)
-        tokens, channels = self.tokens, self.destination.channels
-        if self.destination.token_offset + tokens > self.destination.capacity:
-            raise ConfigurationError("destination slot exceeds the native cache capacity")
-        if isinstance(self.source, DenseSource):
-            if self.basis is not None or self.rank is not None:
-                raise ConfigurationError("dense sources take no basis or rank")
-            if tuple(self.source.values.shape) != (tokens, channels):
-                raise ConfigurationError("dense values must be [tokens, heads * head_dim]")
-        else:
-            basis = _require_tensor(self.basis, "basis")
-            if basis.ndim != 2 or basis.shape[1] != channels:
-                raise ConfigurationError("basis must be [rows, heads * head_dim] of the destination")
-            if basis.dtype not in (torch.float16, torch.bfloat16, torch.float32):
-                raise ConfigurationError("basis must be float16 rows (bfloat16 accepted; float32 for reference use)")
-            if isinstance(self.source, PictureSource):
-                layout = self.source.layout
-                if (layout["frames"], layout["height"], layout["width"]) != grid:
-                    raise ConfigurationError("picture layout geometry differs from the job grid")
-                columns = layout["rank"]
-            else:
-                if self.source.values.shape[0] != tokens:
-                    raise ConfigurationError("coefficient rows differ from the job token count")
-                columns = self.source.values.shape[1]
-            rank = columns if self.rank is None else self.rank
-            _int(rank, "rank", minimum=1)
-            if rank > basis.shape[0]:
-                raise ConfigurationError("rank view exceeds the basis rows")
-            if rank > columns or (isinstance(self.source, PictureSource) and rank != columns):
-                raise ConfigurationError("rank view exceeds the available coefficient columns")
-            object.__setattr__(self, "rank", rank)
-        if self.rope is not None:
-            if not isinstance(self.rope, RopePositions):
-                raise ConfigurationError("rope must be RopePositions")
-            table = self.rope.table
-            if table.head_dim != self.destination.head_dim:
-                raise ConfigurationError("RoPE table pairs differ from head_dim // 2")
-            if table.sections is None:
-                if self.rope.rows + tokens > table.rows:
-                    raise ConfigurationError("dense RoPE rows exceed the table")
-            else:
-                needed = tuple(row + size for row, size in zip(self.rope.rows, grid))
-                if any(need > limit for need, limit, pairs in zip(needed, table.section_rows, table.sections) if pairs):
-                    raise ConfigurationError("separable RoPE rows exceed the table")
-
-    @property
-    def tokens(self):
-        frames, height, width = self.grid
-        return frames * height * width
-
-    @property
-    def channels(self):
-        return self.destination.channels
-
-    def tensors(self):
-        """Every tensor this job reads or writes (for lifetime tracking)."""
-        result = [self.destination.tensor]
-        source = self.source
-        if isinstance(source, PictureSource):
-            result.extend(picture for segment in source.pictures for picture in segment)
-        else:
-            result.append(source.values)
-        if self.basis is not None:
-            result.append(self.basis)
-        if self.rope is not None:
-            result.extend((self.rope.table.cos, self.rope.table.sin))
-        return result
-
-
-# ---------------------------------------------------------------------------
-# Completion handle
-# ---------------------------------------------------------------------------
-
-_DEFERRED: list = []
-_DEFERRED_LOCK = threading.RLock()
-
-
-def _sweep_deferred():
-    """Drop references of collected-but-unreleased handles whose GPU work has finished."""
-    with _DEFERRED_LOCK:
-        if _DEFERRED:
-            _DEFERRED[:] = [(event, refs) for event, refs in _DEFERRED if not event.query()]
-
-
-def pending_deferred():
-    """Number of collected handles whose inputs are still held until their event completes."""
-    with _DEFERRED_LOCK:
-        return len(_DEFERRED)
-
-
-class RestoreHandle:
-    """Completion of one :func:`reconstruct` call.
-
-    ``event`` is recorded on the execution stream after the last write (None for
-    host execution).  The handle keeps all inputs, tables and temporaries alive
-    until :meth:`release`; a handle collected before release parks them until its
-    event completes.
-    """
-
-    def __init__(self, *, event, stream, keepalive, stats):
-        self._event = event
-        self._stream = stream
-        self._keepalive = keepalive
-        self._released = False
-        self.stats = stats
-
-    @property
-    def event(self):
-        return self._event
-
-    @property
-    def stream(self):
-        return self._stream
-
-    @property
-    def released(self):
-        return self._released
-
-    def query(self):
-        return self._event is None or self._event.query()
-
-    def synchronize(self):
-        if self._event is not None:
-            self._event.synchronize()
-
-    def wait(self, stream=None):
-        """Make ``stream`` (default: current) wait for completion without blocking the host."""
-        if self._event is None:
-            return
-        (torch.cuda.current_stream(self._stream.device) if stream is None else stream).wait_event(self._event)
-
-    def release(self):
-        """Wait for completion, then drop every retained input and temporary."""
-        if self._released:
-            return
-        self.synchronize()
-        self._keepalive = None
-        self._released = True
-        _sweep_deferred()
-
-    def __del__(self):
-        try:
-            if not self._released and self._event is not None and self._keepalive is not None:
-                if not self._event.query():
-                    with _DEFERRED_LOCK:
-                        _DEFERRED.append((self._event, self._keepalive))
-        except Exception:  # noqa: BLE001 - interpreter shutdown
-            pass
-
-
-# ---------------------------------------------------------------------------
-# Validation and the reference backend
-# ---------------------------------------------------------------------------
-
-
-def _storage_key(tensor):
-    try:
-        return tensor.untyped_storage().data_ptr(), tensor.device
-    except (RuntimeError, NotImplementedError):
-        return tensor.data_ptr(), tensor.device
-
-
-def _check_disjoint(jobs):
-    """Reject jobs whose slots in the same destination view overlap (concurrent writes would race)."""
-    spans: dict = {}
-    for index, job in enumerate(jobs):
-        view = job.destination
-        tensor = view.tensor
-        key = (*_storage_key(tensor), tensor.storage_offset(), tuple(tensor.shape), tensor.stride(),
-               view.layout, view.batch_index)
-        spans.setdefault(key, []).append((view.token_offset, view.token_offset + job.tokens, index))
-    for intervals in spans.values():
-        intervals.sort()
-        for (_, stop, first), (start, _, second) in zip(intervals, intervals[1:]):
-            if start < stop:
-                raise ConfigurationError(f"jobs {first} and {second} write overlapping destination tokens")
-
-
-def _validate(jobs):
-    if isinstance(jobs, ReconstructionJob):
-        jobs = (jobs,)
-    if not isinstance(jobs, Sequence) or isinstance(jobs, (str, bytes)):
-        raise ConfigurationError("jobs must be a sequence of ReconstructionJob")
-    jobs = tuple(jobs)
-    if any(not isinstance(job, ReconstructionJob) for job in jobs):
-        raise ConfigurationError("jobs must be ReconstructionJob instances")
-    devices = set()
-    for job in jobs:
-        devices.add(job.destination.tensor.device)
-        source = job.source
-        devices.add(source.device if isinstance(source, PictureSource) else source.values.device)
-        if job.basis is not None:
-            devices.add(job.basis.device)
-    if len(devices) > 1:
-        raise ConfigurationError("all job tensors (except RoPE tables) must share one device")
-    _check_disjoint(jobs)
-    return jobs, (devices.pop() if devices else None)
-
-
-def unpack_pictures(source):
-    """Quantized coefficient pixels ``[N, rank]`` of a :class:`PictureSource` (channel_tiles.v1)."""
-    layout = source.layout
-    frames, height, width, rank = layout["frames"], layout["height"], layout["width"], layout["rank"]
-    columns, rows = layout["grid"]
-    planes, slots = layout["planes"], layout["channels_per_segment"]
-    values = torch.empty((frames, height, width, rank), dtype=torch.uint8, device=source.device)
-    for segment, pictures in enumerate(source.pictures):
-        first = segment * slots
-        count = min(slots, rank - first)
-        for frame, picture in enumerate(pictures):
-            # [planes, rows*height, columns*width] -> cells ordered (row, column, plane) per token.
-            cells = picture[:planes, :rows * height, :columns * width].reshape(planes, rows, height, columns, width)
-            values[frame, :, :, first:first + count] = cells.permute(2, 4, 1, 3, 0).reshape(height, width, -1)[..., :count]
-    return values.reshape(-1, rank)
-
-
-def dequantize(pixels, scale, offset):
-    """``float(pixel) * scale + offset`` with the eager rounding (mul, then add)."""
-    scale = torch.from_numpy(np.ascontiguousarray(scale)).to(pixels.device)
-    offset = torch.from_numpy(np.ascontiguousarray(offset)).to(pixels.device)
-    return pixels.float().mul_(scale).add_(offset)
-
-
-def reference_coefficients(job):
-    """The FP32 coefficient matrix ``[N, rank]`` a job reconstructs from."""
-    source = job.source
-    if isinstance(source, PictureSource):
-        return dequantize(unpack_pictures(source), source.scale, source.offset)
-    if isinstance(source, CoefficientSource):
-        if source.quantized:
-            return dequantize(source.values[:, :job.rank], source.scale[:job.rank], source.offset[:job.rank])
-        return source.values[:, :job.rank].float()
-    raise ConfigurationError("dense sources have no coefficients")
-
-
-def rope_cos_sin(positions, grid, *, dtype=torch.float64, device=None):
-    """Per-token ``(cos, sin)`` ``[N, head_dim // 2]`` for a job's positions."""
-    table = positions.table
-    device = table.cos.device if device is None else device
-    cos = table.cos.to(device=device, dtype=dtype)
-    sin = table.sin.to(device=device, dtype=dtype)
-    frames, height, width = grid
-    tokens = frames * height * width
-    if table.sections is None:
-        first = positions.rows
-        return cos[first:first + tokens], sin[first:first + tokens]
-    index = torch.arange(tokens, device=device)
-    plane = height * width
-    axes = (index // plane, (index % plane) // width, index % width)
-    out_cos = torch.empty((tokens, table.pairs), dtype=dtype, device=device)
-    out_sin = torch.empty_like(out_cos)
-    column = 0
-    for axis, pairs in enumerate(table.sections):
-        rows = positions.rows[axis] + axes[axis]
-        out_cos[:, column:column + pairs] = cos[rows, column:column + pairs]
-        out_sin[:, column:column + pairs] = sin[rows, column:column + pairs]
-        column += pairs
-    return out_cos, out_sin
-
-
-def apply_rope_reference(values, positions, grid, *, dtype=torch.float64):
-    """Rotate interleaved pairs of ``values[N, H, D]`` in ``dtype`` (Wan complex product)."""
-    cos, sin = rope_cos_sin(positions, grid, dtype=dtype, device=values.device)
-    x = values.to(dtype)
-    even, odd = x[..., 0::2], x[..., 1::2]
-    cos, sin = cos[:, None, :], sin[:, None, :]
-    out = torch.empty_like(x)
-    out[..., 0::2] = even * cos - odd * sin
-    out[..., 1::2] = even * sin + odd * cos
-    return out
-
-
-def _pre_rope(job, compute):
-    if isinstance(job.source, DenseSource):
-        return job.source.values
-    coefficients = reference_coefficients(job)
-    basis = job.basis[:job.rank]
-    return coefficients.to(compute) @ basis.to(device=coefficients.device, dtype=compute)
-
-
-def fp32_matmul_precision(device_type):
-    """Precision this process lets FP32 torch matmuls on ``"cuda"`` or ``"cpu"`` use (read only)."""
-    holder = torch.backends.cuda.matmul if device_type == "cuda" else getattr(
-        getattr(torch.backends, "mkldnn", None), "matmul", None)
-    precision = getattr(holder, "fp32_precision", None)
-    if isinstance(precision, str):
-        return "ieee" if precision in ("ieee", "none") else precision
-    legacy = torch.get_float32_matmul_precision()
-    return "ieee" if legacy == "highest" else legacy
-
-
-def _require_fp32_matmul(device_type, accepted, what):
-    actual = fp32_matmul_precision(device_type)
-    if actual not in accepted:
-        raise UnsupportedError(
-            f"{what} needs {device_type} FP32 matmuls at {' / '.join(accepted)} precision, but this process set "
-            f"{actual!r}; that setting is process-wide, so restore_kernels never changes it")
-
-
-def _reference_job(job, compute, native_rope, native_rope_dtype):
-    heads, head_dim, tokens = job.destination.heads, job.destination.head_dim, job.tokens
-    slot = job.destination.slot(tokens)
-    values = _pre_rope(job, compute)
-    if native_rope is not None and job.rope is not None:
-        dtype = slot.dtype if native_rope_dtype is None else native_rope_dtype
-        result = native_rope(values.to(dtype).reshape(tokens, heads, head_dim), job)
-        if not isinstance(result, torch.Tensor) or result.numel() != tokens * heads * head_dim:
-            raise IntegrityError("native RoPE callable returned a tensor of the wrong size")
-        slot.copy_(result.reshape(tokens, heads, head_dim))
-        return
-    values = values.reshape(tokens, heads, head_dim)
-    if job.rope is not None:
-        values = apply_rope_reference(values, job.rope, job.grid, dtype=compute)
-    slot.copy_(values)
-
-
-def reconstruct_reference(jobs, *, compute_dtype=torch.float64, native_rope=None, native_rope_dtype=None):
-    """Plain-torch reference: FP64 (default) or IEEE FP32 math, then one cast (runs on the jobs' device)."""
-    jobs, device = _validate(jobs)
-    if compute_dtype not in (torch.float32, torch.float64):
-        raise ConfigurationError("reference compute dtype must be float32 or float64")
-    if compute_dtype == torch.float32 and device is not None:
-        _require_fp32_matmul(device.type, ("ieee",), "the FP32 reference (compute_dtype=torch.float32)")
-    with torch.no_grad():
-        for job in jobs:
-            _reference_job(job, compute_dtype, native_rope, native_rope_dtype)
-
-
-_UNIT_ROUNDOFF = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11, torch.float32: 2.0 ** -24}
-# Smallest-magnitude rounding floor of each output format (half its subnormal spacing).
-_OUTPUT_FLOOR = {torch.bfloat16: 2.0 ** -134, torch.float16: 2.0 ** -25, torch.float32: 2.0 ** -150}
-
-
-def _gemm_gamma(precision, rank):
-    """Relative product error per unit of ``sum_k |a_k| |q_k|`` for each precision mode
-    (reelcache/restore_kernels.py:1176-1187)."""
-    accumulate = (rank + 1) * 2.0 ** -24
-    return {
-        "fp32": accumulate,
-        "tf32": 2.0 ** -10 + accumulate,
-        "tf32x3": 2.0 ** -20 + 3 * accumulate,
-        "fp16": 2.0 ** -11 + accumulate,
-        "fp16x2": 2.0 ** -21 + 2 * accumulate,
-        "bf16": 2.0 ** -7 + 2.0 ** -16 + accumulate,
-        "reference32": accumulate,
-    }[precision]
-
-
-def reference_values(job):
-    """FP64 values ``y*[N, C]`` a job writes before the final cast, and ``sum_k |p_k| |q_k|``."""
-    tokens, heads, head_dim = job.tokens, job.destination.heads, job.destination.head_dim
-    if isinstance(job.source, DenseSource):
-        values = job.source.values.double()
-        magnitude = torch.zeros_like(values)
-    else:
-        coefficients = reference_coefficients(job).double()
-        basis = job.basis[:job.rank].to(device=coefficients.device, dtype=torch.float64)
-        values = coefficients @ basis
-        magnitude = coefficients.abs() @ basis.abs()
-    if job.rope is not None:
-        values = apply_rope_reference(values.reshape(tokens, heads, head_dim), job.rope, job.grid).reshape(tokens, -1)
-        pairs = magnitude.reshape(tokens, -1, 2)
-        magnitude = (pairs[..., 0] + pairs[..., 1]).repeat_interleave(2, dim=-1)
-    return values, magnitude
-
-
-def error_bound(job, precision, out_dtype=None):
-    """Elementwise bound on ``|written - y*|`` for a precision mode (first-order analysis).
-
-    ``|y_hat - y*| <= u_out |y*| + (1 + u_out) E + floor`` with
-    ``E = gamma(precision, rank) * S + 2**-21 (|y_e| + |y_o|)`` (the last term only
-    with RoPE), ``S = sum_k |p_k| |q_k|`` summed over each rotated pair
-    (reelcache/restore_kernels.py:1208-1227).  Returns ``(y*, bound)`` in FP64.
-    """
-    values, magnitude = reference_values(job)
-    out_dtype = job.destination.tensor.dtype if out_dtype is None else out_dtype
-    unit = _UNIT_ROUNDOFF[out_dtype]
-    error = _gemm_gamma(precision, job.rank or 0) * magnitude
-    if job.rope is not None:
-        pairs = values.reshape(job.tokens, -1, 2).abs()
-        error = error + 2.0 ** -21 * (pairs[..., 0] + pairs[..., 1]).repeat_interleave(2, dim=-1)
-    return values, unit * values.abs() + (1 + unit) * error + _OUTPUT_FLOOR[out_dtype]
 
 
 # ---------------------------------------------------------------------------
@@ -1884,51 +946,71 @@ def _merged_config(config):
     return merged
 
 
-def _run_hip(jobs, *, precision, config, stream, device, keepalive, stage_events):
-    plan = _CallPlan(list(jobs), device, stream, precision, config, keepalive)
-    launches = plan.run(stage_events)
-    return launches, plan.grids, plan.variants
+class _null(contextlib.nullcontext):
+    """A context that does nothing (host execution has no stream to enter)."""
 
 
-class _null:
-    def __enter__(self):
-        return self
-
-    def __exit__(self, *_):
-        return False
+def _on(stream):
+    return torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext()
 
 
-def _native_rope_jobs(jobs, native_rope, native_rope_dtype, run, stream, keepalive):
-    """Exact path: reconstruct pre-RoPE K into temporaries, call the engine's RoPE, copy into the slot."""
-    staged, prepared = [], []
-    for job in jobs:
-        heads, head_dim, tokens = job.destination.heads, job.destination.head_dim, job.tokens
-        dtype = job.destination.tensor.dtype if native_rope_dtype is None else native_rope_dtype
-        if isinstance(job.source, DenseSource) and job.source.values.dtype == dtype:
-            prepared.append((job, job.source.values.reshape(tokens, heads, head_dim)))
-            continue
-        if dtype not in OUTPUT_DTYPES:
-            raise ConfigurationError("native RoPE input dtype must be bfloat16, float16 or float32")
-        with torch.cuda.stream(stream) if stream is not None else _null():
-            temporary = torch.empty((tokens, heads, head_dim), dtype=dtype, device=job.destination.tensor.device)
-        keepalive.append(temporary)
-        staged.append(ReconstructionJob(job.source, NativeView(temporary, "THD"), job.grid, job.basis, job.rank, None,
-                                        job.label))
-        prepared.append((job, temporary))
-    launches = run(staged) if staged else 0
-    with torch.cuda.stream(stream) if stream is not None else _null():
-        for job, values in prepared:
-            result = native_rope(values, job)
-            heads, head_dim, tokens = job.destination.heads, job.destination.head_dim, job.tokens
-            if not isinstance(result, torch.Tensor) or result.numel() != tokens * heads * head_dim:
-                raise IntegrityError("native RoPE callable returned a tensor of the wrong size")
-            keepalive.append(result)
-            job.destination.slot(tokens).copy_(result.reshape(tokens, heads, head_dim))
-    return launches
+def _execution_stream(device, stream, wait_events):
+    """The stream a call runs on (``None`` for host execution), after ``wait_events``."""
+    if device.type != "cuda":
+        need(stream is None and not wait_events, "host execution takes no GPU stream or events")
+        return None
+    stream = torch.cuda.current_stream(device) if stream is None else stream
+    need(isinstance(stream, torch.cuda.Stream) and stream.device == device,
+         "stream must be a torch.cuda.Stream on the jobs' device")
+    for event in wait_events:
+        stream.wait_event(event)
+    return stream
 
 
 def _matrix_flops(jobs):
     return sum(2 * job.tokens * job.rank * job.channels for job in jobs if job.rank)
+
+
+class _FusedCall:
+    """The HIP execution of one :func:`reconstruct` call: one :class:`_CallPlan` for the jobs the
+    kernels rotate (or write unrotated) and, with ``native_rope``, one for the pre-RoPE K that the
+    engine's callable rotates before the copy into its slot."""
+
+    def __init__(self, device, stream, precision, config, keepalive, stage_events, stats):
+        self.device, self.stream, self.precision = device, stream, precision
+        self.config, self.keepalive, self.stage_events, self.stats = config, keepalive, stage_events, stats
+        stats.update(grids=[], variants=[])
+
+    def launch(self, jobs):
+        plan = _CallPlan(list(jobs), self.device, self.stream, self.precision, self.config, self.keepalive)
+        self.stats["launches"] += plan.run(self.stage_events)
+        self.stats["grids"].extend(plan.grids)
+        self.stats["variants"].extend(plan.variants)
+
+    def rotate_natively(self, jobs, native_rope, native_rope_dtype):
+        """Exact path: pre-RoPE K into THD temporaries (a dense source already in the rotation
+        dtype is used as is), the engine's rotation, then a copy into each slot."""
+        need(native_rope_dtype is None or native_rope_dtype in OUTPUT_DTYPES,
+             "native RoPE input dtype must be bfloat16, float16 or float32")
+        inputs, staged = [], []
+        for job in jobs:
+            view = job.destination
+            shape = (job.tokens, view.heads, view.head_dim)
+            dtype = native_rope_dtype or view.tensor.dtype
+            if isinstance(job.source, DenseSource) and job.source.values.dtype == dtype:
+                inputs.append(job.source.values.reshape(shape))
+                continue
+            temporary = torch.empty(shape, dtype=dtype, device=view.tensor.device)
+            self.keepalive.append(temporary)
+            staged.append(ReconstructionJob(job.source, NativeView(temporary, "THD"), job.grid, job.basis, job.rank,
+                                            None, job.label))
+            inputs.append(temporary)
+        if staged:
+            self.launch(staged)
+        for job, values in zip(jobs, inputs):
+            rotated = _native_rotation(native_rope, values, job, values.dtype)
+            self.keepalive.append(rotated)
+            job.destination.slot(job.tokens).copy_(rotated)
 
 
 def reconstruct(jobs, *, backend="auto", precision="auto", stream=None, wait_events=(), native_rope=None,
@@ -1943,283 +1025,56 @@ def reconstruct(jobs, *, backend="auto", precision="auto", stream=None, wait_eve
     ``stream``: torch stream to run on (default: current), after ``wait_events``.
     ``native_rope``: optional ``(pre_rope[N, H, D], job) -> post_rope`` used instead
     of the built-in rotation for jobs with RoPE.  ``config``: launch overrides
-    (``workgroups_per_cu``, ``store_cost``).  ``stage_events``: optional list
-    receiving ``(stage, event)`` timing events ("start", "pack", "launch<n>" after the n-th launch of the
-    call, "fused", "rope_store").
+    (``workgroups_per_cu``, ``store_cost``, kernel-variant switches).  ``stage_events``: optional
+    list receiving ``(stage, event)`` timing events ("start", "pack", "launch<n>" after the n-th
+    launch of the call, "fused", "rope_store").
 
     Returns a :class:`RestoreHandle`; destinations are valid after its event.
     """
     _sweep_deferred()
     jobs, device = _validate(jobs)
-    if backend not in BACKENDS:
-        raise ConfigurationError(f"backend must be one of {BACKENDS}")
-    if precision != "auto" and precision not in PRECISIONS:
-        raise ConfigurationError(f"precision must be 'auto' or one of {PRECISIONS}")
-    if native_rope is not None and not callable(native_rope):
-        raise ConfigurationError("native_rope must be callable")
+    need(backend in BACKENDS, f"backend must be one of {BACKENDS}")
+    need(precision == "auto" or precision in PRECISIONS, f"precision must be 'auto' or one of {PRECISIONS}")
+    need(native_rope is None or callable(native_rope), "native_rope must be callable")
     stats = {"jobs": len(jobs), "matrices": len(jobs), "flops": _matrix_flops(jobs), "launches": 0}
     if not jobs:
         stats.update(backend="none", precision=None)
         return RestoreHandle(event=None, stream=None, keepalive=None, stats=stats)
-    cuda = device.type == "cuda"
-    resolved = _resolve_backend(backend, cuda)
+    resolved = _resolve_backend(backend, device.type == "cuda")
     if resolved == "reference":
-        if compute_dtype not in (torch.float32, torch.float64):
-            raise ConfigurationError("reference compute dtype must be float32 or float64")
-        if compute_dtype == torch.float32:
-            _require_fp32_matmul(device.type, ("ieee",), "the FP32 reference (compute_dtype=torch.float32)")
+        _check_compute_dtype(compute_dtype, device)
+        label = str(compute_dtype)
     else:
-        precision = _resolve_precision(precision, device)
-    if cuda:
-        stream = torch.cuda.current_stream(device) if stream is None else stream
-        if not isinstance(stream, torch.cuda.Stream) or stream.device != device:
-            raise ConfigurationError("stream must be a torch.cuda.Stream on the jobs' device")
-    elif stream is not None or wait_events:
-        raise ConfigurationError("host execution takes no GPU stream or events")
+        precision = label = _resolve_precision(precision, device)
+    stream = _execution_stream(device, stream, wait_events)
     keepalive = [tensor for job in jobs for tensor in job.tensors()]
-    stats.update(backend=resolved, precision=precision if resolved != "reference" else str(compute_dtype),
-                 picture_path="fused_gather" if resolved == "fused" else resolved)
-    if cuda:
-        for event in wait_events:
-            stream.wait_event(event)
+    stats.update(backend=resolved, precision=label, picture_path="fused_gather" if resolved == "fused" else resolved)
     if resolved == "reference":
-        with torch.cuda.stream(stream) if cuda else _null():
+        with _on(stream):
             reconstruct_reference(jobs, compute_dtype=compute_dtype, native_rope=native_rope,
                                   native_rope_dtype=native_rope_dtype)
     else:
-        merged = _merged_config(config)
-        grids, variants = [], []
-
-        def run(selected):
-            launches, group_grids, group_variants = _run_hip(selected, precision=precision, config=merged,
-                                                             stream=stream, device=device, keepalive=keepalive,
-                                                             stage_events=stage_events)
-            grids.extend(group_grids)
-            variants.extend(group_variants)
-            return launches
-
-        exact = [job for job in jobs if native_rope is not None and job.rope is not None]
-        ordinary = [job for job in jobs if not (native_rope is not None and job.rope is not None)]
+        call = _FusedCall(device, stream, precision, _merged_config(config), keepalive, stage_events, stats)
+        native = [job for job in jobs if native_rope is not None and job.rope is not None]
+        fused = [job for job in jobs if native_rope is None or job.rope is None]
         try:
             with torch.cuda.stream(stream):
-                if ordinary:
-                    stats["launches"] += run(ordinary)
-                if exact:
-                    stats["launches"] += _native_rope_jobs(exact, native_rope, native_rope_dtype, run, stream,
-                                                           keepalive)
+                if fused:
+                    call.launch(fused)
+                if native:
+                    call.rotate_natively(native, native_rope, native_rope_dtype)
         except BaseException:
-            failed = torch.cuda.Event()
-            failed.record(stream)
-            with _DEFERRED_LOCK:
-                _DEFERRED.append((failed, keepalive))
+            park_failed(stream, keepalive)
             raise
-        stats["grids"] = grids
-        stats["variants"] = variants
     event = None
-    if cuda:
+    if stream is not None:
         event = torch.cuda.Event()
         event.record(stream)
     return RestoreHandle(event=event, stream=stream, keepalive=keepalive, stats=stats)
 
 
-# ---------------------------------------------------------------------------
-# Warm-up
-# ---------------------------------------------------------------------------
-
-WARMUP_SOURCES = ("pictures", "uint8", "float", "dense")
-WARMUP_ROPE_MODES = ("none", "fused", "native")
-_WARMUP_GRID = (1, 4, 8)
-_WARMUP_MAX_RANK = 65536
-_WARMUP_LOCK = threading.Lock()
-_WARMED: set = set()
-
-
-@dataclass(frozen=True)
-class WarmupShape:
-    """One kind of launch group of the restore path (see :func:`warmup`)."""
-
-    heads: int
-    head_dim: int
-    dtype: torch.dtype = torch.bfloat16
-    layout: str = "BTHD"
-    source: str = "pictures"
-    rope: str = "fused"
-    ranks: tuple = (1, 1024)
-    source_dtype: torch.dtype | None = None
-    native_rope_dtype: torch.dtype | None = None
-
-    def __post_init__(self):
-        _int(self.heads, "heads", minimum=1)
-        _int(self.head_dim, "head_dim", minimum=1)
-        if self.dtype not in OUTPUT_DTYPES:
-            raise ConfigurationError(f"warm-up cache dtype must be one of {OUTPUT_DTYPES}")
-        if self.layout not in LAYOUTS:
-            raise ConfigurationError(f"warm-up layout must be one of {LAYOUTS}")
-        if self.source not in WARMUP_SOURCES:
-            raise ConfigurationError(f"warm-up source must be one of {WARMUP_SOURCES}")
-        if self.rope not in WARMUP_ROPE_MODES:
-            raise ConfigurationError(f"warm-up rope must be one of {WARMUP_ROPE_MODES}")
-        if self.rope != "none" and self.head_dim % 2:
-            raise ConfigurationError("RoPE needs an even head_dim")
-        ranks = tuple(self.ranks) if isinstance(self.ranks, Sequence) and not isinstance(self.ranks, str) else ()
-        if len(ranks) != 2:
-            raise ConfigurationError("ranks must be (minimum, maximum)")
-        low = _int(ranks[0], "minimum rank", minimum=1)
-        high = _int(ranks[1], "maximum rank", minimum=low)
-        if high > _WARMUP_MAX_RANK:
-            raise ConfigurationError(f"warm-up ranks above {_WARMUP_MAX_RANK} are not supported")
-        object.__setattr__(self, "ranks", (low, high))
-        if self.source in ("float", "dense"):
-            if self.source_dtype is not None and self.source_dtype not in COEFFICIENT_DTYPES:
-                raise ConfigurationError(f"source_dtype must be one of {COEFFICIENT_DTYPES}")
-        elif self.source_dtype is not None:
-            raise ConfigurationError("source_dtype applies to float and dense sources only")
-        if self.native_rope_dtype is not None:
-            if self.rope != "native":
-                raise ConfigurationError("native_rope_dtype applies to rope='native' only")
-            if self.native_rope_dtype not in OUTPUT_DTYPES:
-                raise ConfigurationError(f"native_rope_dtype must be one of {OUTPUT_DTYPES}")
-
-    def describe(self):
-        return {"heads": self.heads, "head_dim": self.head_dim, "dtype": str(self.dtype), "layout": self.layout,
-                "source": self.source, "rope": self.rope, "ranks": list(self.ranks),
-                "source_dtype": None if self.source_dtype is None else str(self.source_dtype),
-                "native_rope_dtype": None if self.native_rope_dtype is None else str(self.native_rope_dtype)}
-
-
-# Register-resident rank steps of the compiled variants (their code objects load on first launch):
-# the one-wave classes, the rank-halves classes and the chunked general kernel beyond them.
-_VARIANT_STEPS = (2, 4, 8, 12, 16, 24, 32, 33)
-
-
-def _warmup_ranks(ranks):
-    """One rank per compiled variant class reachable within ``ranks``."""
-    low, high = ranks
-    chosen = []
-    for steps in _VARIANT_STEPS:
-        rank = min(high, 16 * steps)
-        if rank >= low and rank not in chosen:
-            chosen.append(rank)
-        if 16 * steps >= high:
-            break
-    return chosen or [high]
-
-
-def _warmup_jobs(shape, rank, device):
-    from .quantize import video_layout
-
-    tokens = math.prod(_WARMUP_GRID)
-    targets = ("K", "V") if shape.rope != "none" else ("V",)
-    sizes = {"BTHD": (1, tokens * len(targets), shape.heads, shape.head_dim),
-             "THD": (tokens * len(targets), shape.heads, shape.head_dim),
-             "BHTD": (1, shape.heads, tokens * len(targets), shape.head_dim)}[shape.layout]
-    destination = torch.zeros(sizes, dtype=shape.dtype, device=device)
-    channels = shape.heads * shape.head_dim
-    basis = None if shape.source == "dense" else torch.zeros((rank, channels), dtype=torch.float16, device=device)
-    table = None
-    if shape.rope != "none":
-        cos = torch.ones((tokens, shape.head_dim // 2), dtype=torch.float32, device=device)
-        table = RopeTable.from_cos_sin(cos, torch.zeros_like(cos))
-    jobs = []
-    for position, target in enumerate(targets):
-        view = NativeView(destination, shape.layout, token_offset=position * tokens)
-        scale, offset = np.full(rank, 1 / 255, dtype=np.float32), np.zeros(rank, dtype=np.float32)
-        if shape.source == "dense":
-            source = DenseSource(torch.zeros((tokens, channels), dtype=shape.source_dtype or shape.dtype,
-                                             device=device))
-        elif shape.source == "float":
-            source = CoefficientSource(torch.zeros((tokens, rank), dtype=shape.source_dtype or torch.float32,
-                                                   device=device))
-        elif shape.source == "uint8":
-            source = CoefficientSource(torch.zeros((tokens, rank), dtype=torch.uint8, device=device), scale, offset)
-        else:
-            layout = video_layout(*_WARMUP_GRID, rank, "yuv444p")
-            frames = layout["frames"]
-            canvases = torch.zeros((layout["segments"] * frames, layout["planes"], layout["image_height"],
-                                    layout["image_width"]), dtype=torch.uint8, device=device)
-            indices = [[segment * frames + frame for frame in range(frames)] for segment in range(layout["segments"])]
-            source = PictureSource.from_canvases(canvases, layout, indices, (0, 0), scale, offset)
-        jobs.append(ReconstructionJob(source, view, _WARMUP_GRID, basis=basis,
-                                      rank=None if shape.source == "dense" else rank,
-                                      rope=RopePositions(table, 0) if target == "K" else None,
-                                      label=f"warmup:{target}:{rank}"))
-    return jobs
-
-
-def _identity_rope(values, job):
-    """Stands in for the engine's ``native_rope`` callable during :func:`warmup`."""
-    return values
-
-
-def warmup(device, shapes, *, backend="auto", precision="auto", config=None, stream=None):
-    """Load every kernel variant :func:`reconstruct` launches for ``shapes`` before the first restore.
-
-    The HIP kernels are compiled ahead of time, so warming up loads their code
-    objects and runs one tiny synthetic call per reachable variant (rank class x
-    precision) through the real launch path.  Serialized by a lock; repeat calls
-    for a warmed (device, shape, backend, precision, config) do no work.
-    Returns a report (``seconds``, ``calls``, ``launches``, per-shape entries).
-    """
-    started = time.perf_counter()
-    if isinstance(shapes, (WarmupShape, Mapping)):
-        shapes = [shapes]
-    shapes = [shape if isinstance(shape, WarmupShape) else WarmupShape(**shape) for shape in shapes]
-    if not shapes:
-        raise ConfigurationError("warmup needs at least one WarmupShape")
-    if backend not in BACKENDS:
-        raise ConfigurationError(f"backend must be one of {BACKENDS}")
-    device = torch.device(device)
-    cuda = device.type == "cuda"
-    resolved = _resolve_backend(backend, cuda)
-    if cuda and device.index is None:
-        device = torch.device("cuda", torch.cuda.current_device())
-    names = [precision] if isinstance(precision, str) else list(precision)
-    if not names:
-        raise ConfigurationError("warmup needs at least one precision")
-    report = {"device": str(device), "backend": backend, "resolved_backend": resolved, "precisions": [],
-              "repeat": False, "warmed": 0, "skipped": 0, "calls": 0, "launches": 0, "shapes": []}
-    if resolved == "reference":
-        report.update(seconds=time.perf_counter() - started, note="the reference backend compiles no kernels")
-        return report
-    precisions = []
-    for name in names:
-        if name != "auto" and name not in PRECISIONS:
-            raise ConfigurationError(f"precision must be 'auto' or one of {PRECISIONS}")
-        name = _resolve_precision(name, device)
-        if name not in precisions:
-            precisions.append(name)
-    report["precisions"] = precisions
-    merged = _merged_config(config)
-    config_key = tuple(sorted((name, repr(value)) for name, value in merged.items()))
-    with _WARMUP_LOCK, torch.cuda.device(device), (torch.cuda.stream(stream) if stream is not None else _null()):
-        for shape in shapes:
-            for name in precisions:
-                key = (str(device), backend, name, shape, config_key)
-                ranks = [None] if shape.source == "dense" else _warmup_ranks(shape.ranks)
-                entry = {"shape": shape.describe(), "precision": name, "ranks": ranks, "calls": 0, "launches": 0,
-                         "seconds": 0.0, "repeat": key in _WARMED}
-                if entry["repeat"]:
-                    report["skipped"] += 1
-                    report["shapes"].append(entry)
-                    continue
-                shape_started = time.perf_counter()
-                for rank in ranks:
-                    jobs = _warmup_jobs(shape, rank or 1, device)
-                    handle = reconstruct(jobs, backend=backend, precision=name, stream=stream, config=config,
-                                         native_rope=_identity_rope if shape.rope == "native" else None,
-                                         native_rope_dtype=shape.native_rope_dtype)
-                    handle.release()
-                    entry["calls"] += 1
-                    entry["launches"] += handle.stats["launches"]
-                entry["seconds"] = time.perf_counter() - shape_started
-                _WARMED.add(key)
-                report["warmed"] += 1
-                report["calls"] += entry["calls"]
-                report["launches"] += entry["launches"]
-                report["shapes"].append(entry)
-    report["repeat"] = report["warmed"] == 0
-    report["seconds"] = time.perf_counter() - started
-    return report
+# Warm-up: :mod:`reelcache_amd.restore_warmup` (it calls back into :func:`reconstruct`).
+from .restore_warmup import WARMUP_ROPE_MODES, WARMUP_SOURCES, WarmupShape, warmup  # noqa: E402
 
 
 __all__ = [
