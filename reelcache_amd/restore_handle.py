@@ -41,15 +41,16 @@ class _Parking:
         self._holds: list = []
 
     def park(self, hold):
-        if hold.done():
+        if not _capturing() and hold.done():
             return
         with self._lock:
             self._holds.append(hold)
 
     def sweep(self):
-        """Drop every hold whose event has completed; returns how many remain."""
+        """Drop every hold whose event has completed; returns how many remain.  Nothing is
+        queried while this thread's stream captures a HIP graph (a capture forbids it)."""
         with self._lock:
-            if self._holds:
+            if self._holds and not _capturing():
                 self._holds = [hold for hold in self._holds if not hold.done()]
             return len(self._holds)
 
@@ -59,6 +60,10 @@ class _Parking:
 
 
 _PARKING = _Parking()
+
+
+def _capturing():
+    return torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
 
 
 def _sweep_deferred():

@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import math
 import threading
+import weakref
 from collections.abc import Mapping
 from dataclasses import dataclass, field
 from typing import Any
@@ -182,7 +183,7 @@ class _DeviceTable:
     has been observed complete, when the pinned source is dropped as well).  ``stamp`` is the
     table state the block was made from."""
 
-    __slots__ = ("block", "cos", "pairs", "pinned", "ready", "sin", "stamp")
+    __slots__ = ("__weakref__", "block", "cos", "pairs", "pinned", "ready", "sin", "stamp")
 
     def __init__(self, cos, sin, device, stream, stamp):
         rows, width = cos.shape
@@ -214,15 +215,38 @@ class _DeviceTable:
                     _fill(views, cos, sin)
                 self.ready = torch.cuda.Event()
                 self.ready.record(work)
+            _PENDING_TABLES.add(self)
 
     def fence(self, device, stream):
         """Order ``stream`` (default: the current one) after the block's writes."""
         if self.ready is None:
             return
+        if torch.cuda.is_current_stream_capturing():
+            # A capture can neither query the upload's event nor wait on work outside the graph.
+            raise ConfigurationError("a RoPE table's device copy was still pending when the capture began: call "
+                                     "reserve_capture_staging() after the table's first use and before capturing")
         if self.ready.query():
-            self.ready = self.pinned = None
+            self.settle()
             return
         (torch.cuda.current_stream(device) if stream is None else stream).wait_event(self.ready)
+
+    def settle(self):
+        """Wait (host) for the block's writes; afterwards no consumer needs to wait for them."""
+        if self.ready is not None:
+            self.ready.synchronize()
+        self.ready = self.pinned = None
+        _PENDING_TABLES.discard(self)
+
+
+# Device tables whose upload has not been observed complete (settled before HIP-graph captures).
+_PENDING_TABLES: weakref.WeakSet = weakref.WeakSet()
+
+
+def settle_table_uploads():
+    """Wait for every pending RoPE-table upload, so that calls captured afterwards need no
+    ordering against them (a capture cannot query or wait on work outside its graph)."""
+    for table in list(_PENDING_TABLES):
+        table.settle()
 
 
 def _table_device(device):
@@ -338,7 +362,8 @@ class RopeTable:
         """Drop the cached device copies (after updating inference-tensor tables in place)."""
         self._device_cache.clear()
 
-    def _entry(self, device, stream):
+    def _kernel_block(self, device, stream):
+        """The table's :class:`_DeviceTable` on ``device``, ordered before work enqueued next on ``stream``."""
         device = _table_device(device)
         stamp = self._stamp()
         entry = self._device_cache.get(device)
@@ -349,13 +374,13 @@ class RopeTable:
 
     def kernel_tables(self, device, stream=None):
         """Contiguous float32 ``(cos, sin)`` on ``device``, valid for work enqueued next on ``stream``."""
-        entry = self._entry(device, stream)
+        entry = self._kernel_block(device, stream)
         return entry.cos, entry.sin
 
     def kernel_pairs(self, device, stream=None):
         """Interleaved float32 ``[rows, pairs, 2]`` (cos, sin) on ``device``, valid for work enqueued
         next on ``stream`` (built with :meth:`kernel_tables`' copies and ordered by the same event)."""
-        return self._entry(device, stream).pairs
+        return self._kernel_block(device, stream).pairs
 
 
 @dataclass(frozen=True, eq=False)

@@ -41,40 +41,55 @@ def _storage_key(tensor):
     return address, tensor.device
 
 
-def _destination_identity(view):
-    """Jobs write the same token axis exactly when these agree."""
-    tensor = view.tensor
-    return (*_storage_key(tensor), tensor.storage_offset(), tuple(tensor.shape), tensor.stride(), view.layout,
-            view.batch_index)
+class _Facts:
+    """What call validation needs of a job, computed once per job object (jobs are immutable):
+    the devices of its tensors, its destination view's geometry, its token span and its
+    matrix-product flops."""
+
+    __slots__ = ("devices", "dst", "flops", "shift", "span", "view")
+
+    def __init__(self, job):
+        view, source = job.destination, job.source
+        tensor = self.dst = view.tensor
+        devices = {tensor.device, source.device if isinstance(source, PictureSource) else source.values.device}
+        if job.basis is not None:
+            devices.add(job.basis.device)
+        self.devices = devices
+        self.shift = tensor.storage_offset() * tensor.element_size()
+        self.view = (tensor.storage_offset(), tuple(tensor.shape), tensor.stride(), view.layout, view.batch_index,
+                     tensor.device)
+        self.span = (view.token_offset, view.token_offset + job.tokens)
+        self.flops = 2 * job.tokens * job.rank * view.channels if job.rank else 0
 
 
-def _check_disjoint(jobs):
+def _facts(job):
+    facts = job.__dict__.get("_facts")
+    if facts is None:
+        facts = _Facts(job)
+        object.__setattr__(job, "_facts", facts)
+    return facts
+
+
+def _check_disjoint(jobs, facts=None):
     """Reject jobs whose slots in the same destination view overlap (concurrent writes would race)."""
-    by_view: dict = {}
-    for index, job in enumerate(jobs):
-        by_view.setdefault(_destination_identity(job.destination), []).append(index)
-    for members in by_view.values():
+    facts = [_facts(job) for job in jobs] if facts is None else facts
+    views: dict = {}
+    for index, fact in enumerate(facts):
+        # Views of one storage share its base address (data address less the view's offset).
+        views.setdefault((fact.dst.data_ptr() - fact.shift, fact.view), []).append(index)
+    for members in views.values():
         if len(members) < 2:
             continue
-        starts = np.array([jobs[i].destination.token_offset for i in members], dtype=np.int64)
-        stops = starts + np.array([jobs[i].tokens for i in members], dtype=np.int64)
-        order = np.argsort(starts, kind="stable")
-        # Slot k overlaps an earlier one exactly when it starts before the furthest earlier stop.
-        reach = np.maximum.accumulate(stops[order])
-        clash = np.flatnonzero(starts[order][1:] < reach[:-1])
-        if clash.size:
-            later = order[clash[0] + 1]
-            earlier = order[int(np.argmax(stops[order][:clash[0] + 1]))]
-            first, second = sorted((members[earlier], members[later]))
-            raise ConfigurationError(f"jobs {first} and {second} write overlapping destination tokens")
-
-
-def _job_devices(job):
-    source = job.source
-    yield job.destination.tensor.device
-    yield source.device if isinstance(source, PictureSource) else source.values.device
-    if job.basis is not None:
-        yield job.basis.device
+        # Sweep the slots in start order, keeping the one that reaches furthest so far.
+        ordered = sorted(members, key=lambda index: facts[index].span)
+        reach, holder = facts[ordered[0]].span[1], ordered[0]
+        for index in ordered[1:]:
+            start, stop = facts[index].span
+            if start < reach:
+                first, second = sorted((holder, index))
+                raise ConfigurationError(f"jobs {first} and {second} write overlapping destination tokens")
+            if stop > reach:
+                reach, holder = stop, index
 
 
 def _validate(jobs):
@@ -85,9 +100,10 @@ def _validate(jobs):
          "jobs must be a sequence of ReconstructionJob")
     jobs = tuple(jobs)
     need(all(isinstance(job, ReconstructionJob) for job in jobs), "jobs must be ReconstructionJob instances")
-    devices = {device for job in jobs for device in _job_devices(job)}
+    facts = [_facts(job) for job in jobs]
+    devices = set().union(*(fact.devices for fact in facts)) if facts else set()
     need(len(devices) <= 1, "all job tensors (except RoPE tables) must share one device")
-    _check_disjoint(jobs)
+    _check_disjoint(jobs, facts)
     return jobs, next(iter(devices), None)
 
 

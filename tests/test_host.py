@@ -15,6 +15,7 @@ from oracle import quantize as oq
 from oracle import restore as orc
 from reelcache_amd import _lib, quantize as pq
 from reelcache_amd import restore_kernels as rk
+from reelcache_amd import restore_plan as rp
 from reelcache_amd.errors import ConfigurationError, IntegrityError, UnsupportedError
 
 from restore_cases import make_case, written
@@ -268,34 +269,41 @@ def test_vectorized_coefficient_bounds_match_the_per_job_rule():
 
 
 def test_captured_calls_need_reserved_staging(monkeypatch):
-    monkeypatch.setattr(rk, "_STAGING", {})
+    monkeypatch.setattr(rp, "_STAGING", {})
     with pytest.raises(ConfigurationError, match="reserve_capture_staging"):
-        rk._capture_staging(4096)
+        rp._capture_staging(4096)
     slab = torch.zeros(1 << 12, dtype=torch.uint8)
-    monkeypatch.setattr(rk, "_STAGING", {"slab": [slab, 0]})
-    first = rk._capture_staging(1000)
-    second = rk._capture_staging(1000)
+    monkeypatch.setattr(rp, "_STAGING", {"slab": [slab, 0]})
+    first = rp._capture_staging(1000)
+    second = rp._capture_staging(1000)
     assert first.numel() == second.numel() == 1000
     assert second.data_ptr() - slab.data_ptr() == 1024  # regions start 256-byte aligned
     with pytest.raises(ConfigurationError):
-        rk._capture_staging(3000)  # 2048 + 3000 exceeds the 4096-byte slab
+        rp._capture_staging(3000)  # 2048 + 3000 exceeds the 4096-byte slab
 
 
 def test_replaced_staging_slab_stays_alive(monkeypatch):
     """A slab that handed out regions to captured calls is kept when a larger one replaces it
     (captured graphs copy from those regions on every replay)."""
-    monkeypatch.setattr(rk, "_STAGING", {})
-    monkeypatch.setattr(rk, "_RETIRED_SLABS", [])
-    monkeypatch.setattr(rk, "_pinned_bytes", lambda n: torch.zeros(n, dtype=torch.uint8))
-    monkeypatch.setattr(rk.torch.cuda, "is_available", lambda: False)
-    rk.reserve_capture_staging(1 << 20)
-    first_slab = rk._STAGING["slab"][0]
-    region = rk._capture_staging(1 << 19)
-    rk.reserve_capture_staging(1 << 20)  # does not fit the rest of the first slab: a new slab
-    assert rk._STAGING["slab"][0] is not first_slab
-    assert any(kept is first_slab for kept in rk._RETIRED_SLABS)
+    monkeypatch.setattr(rp, "_STAGING", {})
+    monkeypatch.setattr(rp, "_RETIRED_SLABS", [])
+    monkeypatch.setattr(rp, "_pinned_bytes", lambda n: torch.zeros(n, dtype=torch.uint8))
+    monkeypatch.setattr(rp.torch.cuda, "is_available", lambda: False)
+    rp.reserve_capture_staging(1 << 20)
+    first_slab = rp._STAGING["slab"][0]
+    region = rp._capture_staging(1 << 19)
+    rp.reserve_capture_staging(1 << 20)  # does not fit the rest of the first slab: a new slab
+    assert rp._STAGING["slab"][0] is not first_slab
+    assert any(kept is first_slab for kept in rp._RETIRED_SLABS)
     assert region.data_ptr() == first_slab.data_ptr()
     # An unused slab is simply replaced (nothing captured reads it).
-    unused = rk._STAGING["slab"][0]
-    rk.reserve_capture_staging(1 << 21)
-    assert not any(kept is unused for kept in rk._RETIRED_SLABS)
+    unused = rp._STAGING["slab"][0]
+    rp.reserve_capture_staging(1 << 21)
+    assert not any(kept is unused for kept in rp._RETIRED_SLABS)
+
+
+def test_vectorized_prescale_exponents_match_the_scalar_rule():
+    rng = np.random.default_rng(29)
+    bounds = np.concatenate([[0.0, -1.0, 2.0 ** -140, 1.0, 0.5, 2.0 ** 13, 2.0 ** 14, 3.0e38, 1e-45, 16383.999],
+                             rng.lognormal(0, 20, size=2000)])
+    np.testing.assert_array_equal(rp._prescale_exponents(bounds), [rk._prescale_exponent(b) for b in bounds])
