@@ -59,20 +59,29 @@ def layer_bytes():
     return written, written + codes + basis + affine
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "restore_causvid_traffic.md")
+COUNTER_PROFILE = os.path.join(ROOT, "profiles", "restore_causvid_counters.md")
 
 
-def measured_traffic():
-    """HBM bytes per layer call from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
-    (copy-calibrated counters; counters cannot be read from inside this process), or None."""
+def profile_figures():
+    """``{name: value}`` of the machine-readable lines of the committed rocprofv3 summary of the
+    restore kernels (copy-calibrated FETCH_SIZE + WRITE_SIZE per launch, trace durations, MFMA
+    busy); counters cannot be read from inside this process.  Empty when the file is absent."""
+    figures = {}
     try:
-        text = open(TRAFFIC_PROFILE).read()
+        lines = open(COUNTER_PROFILE).read().splitlines()
     except OSError:
-        return None
-    for line in text.splitlines():
-        if line.startswith("traffic_bytes_per_layer_call:"):
-            return int(line.split(":", 1)[1])
-    return None
+        return figures
+    for line in lines:
+        name, _, value = line.partition(":")
+        if name.startswith(("traffic_bytes_per_", "trace_us ", "mfma_busy ")) and value.strip():
+            figures[name] = float(value)
+    return figures
+
+
+def launch_bytes(rank):
+    """Algorithmic bytes of one restore launch (the 7 jobs of one target): codes, basis and affine
+    read, slots written."""
+    return CHUNKS * TOKENS * rank + rank * CHANNELS * 2 + CHUNKS * rank * 8 + CHUNKS * TOKENS * CHANNELS * 2
 
 
 def layer_flops():
@@ -136,42 +145,89 @@ def restore_step(layers, stream, events=None, precision="auto"):
     return handles
 
 
+def cpu_model():
+    """The host CPU's model name (from /proc/cpuinfo), or the platform's processor string."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def host_threads():
+    """BLAS threads for the all-threads CPU baselines: the process's OMP_NUM_THREADS share when set
+    (the GPU boxes set it to their CPU share), else os.cpu_count()."""
+    cores = os.cpu_count() or 1
+    try:
+        return max(1, min(cores, int(os.environ.get("OMP_NUM_THREADS", cores))))
+    except ValueError:
+        return cores
+
+
+def _timed_variants(run_one, budget, variants):
+    """Run ``run_one(compute)`` repeatedly per (label, compute dtype, BLAS threads) variant for
+    about ``budget / len(variants)`` seconds each (at least once); ``{label: (units, seconds)}``."""
+    from threadpoolctl import threadpool_limits
+
+    results = {}
+    share = budget / len(variants)
+    for label, compute, threads in variants:
+        with threadpool_limits(limits=threads):
+            units, started = 0, time.perf_counter()
+            while True:
+                run_one(compute)
+                units += 1
+                elapsed = time.perf_counter() - started
+                if elapsed >= share:
+                    break
+        results[label] = (units, elapsed)
+    return results
+
+
 def cpu_baseline(seconds_budget=20.0, seed=1):
-    """The oracle's CPU restatement of the reference restore (IEEE FP32 product, FP64 RoPE,
-    one bf16 cast) on a bounded sample: whole CausVid layers, as many as fit the budget."""
+    """The oracle's CPU restatement of the reference restore (``reconstruct_reference``: dequantize,
+    the product in FP64 -- the reference's default -- or IEEE FP32, RoPE in the same precision, one
+    bf16 cast) on a bounded sample of CausVid jobs (one chunk's K or V matrix each), with all host
+    threads and with one BLAS thread."""
     from oracle import restore as orc
     from oracle.quantize import covering_affine as cover
 
     rng = np.random.default_rng(seed)
-    threads = os.cpu_count() or 1
+    cores = host_threads()
     basis = {rank: np.linalg.qr(rng.standard_normal((CHANNELS, rank)))[0].T.astype(np.float32)
              for rank in (RANK_K, RANK_V)}
     cos, sin = np.real(orc.wan_freqs(HEAD_DIM, 64)), np.imag(orc.wan_freqs(HEAD_DIM, 64))
     jobs = []
-    for chunk in range(CHUNKS):
+    for chunk in range(2):
         for rank, rope in ((RANK_K, True), (RANK_V, False)):
             codes = rng.integers(0, 256, size=(TOKENS, rank), dtype=np.uint8)
             lo = rng.uniform(-4, 0, size=rank).astype(np.float32)
             affine = cover(lo, (lo + rng.uniform(0.5, 6, size=rank)).astype(np.float32))
             jobs.append((codes, affine, rank, orc.rope_cos_sin(cos, sin, orc.wan_sections(HEAD_DIM // 2),
                                                                (GRID[0] * chunk, 0, 0), GRID) if rope else None))
-    written, _ = layer_bytes()
-    layers = 0
-    started = time.perf_counter()
-    while True:
-        for codes, affine, rank, rope in jobs:
-            coefficients = orc.dequantize(codes, affine[0], affine[1])
-            values = orc.reconstruct(coefficients, basis[rank], HEADS, rope, compute=np.float32)
-            orc.f32_to_bf16_bits(values.astype(np.float32))
-        layers += 1
-        elapsed = time.perf_counter() - started
-        if elapsed >= seconds_budget or layers >= 4:
-            break
-    return {"value": round(layers * written / elapsed / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "port",
-            "sample": f"{layers} CausVid layer(s) (7 chunks x K/V, 4680x1536, r 128/192) through oracle.restore "
-                      f"(numpy FP32 GEMM with BLAS threads, FP64 RoPE, bf16 cast) on {threads} host threads; "
-                      f"{elapsed:.1f} s, {elapsed / layers * 1e3:.0f} ms/layer"}
+    cursor = [0]
+
+    def one_job(compute):
+        codes, affine, rank, rope = jobs[cursor[0] % len(jobs)]
+        cursor[0] += 1
+        coefficients = orc.dequantize(codes, affine[0], affine[1])
+        values = orc.reconstruct(coefficients, basis[rank], HEADS, rope, compute=compute)
+        orc.f32_to_bf16_bits(values.astype(np.float32))
+
+    variants = [("fp64_all_threads", np.float64, cores), ("fp32_all_threads", np.float32, cores),
+                ("fp64_1_thread", np.float64, 1), ("fp32_1_thread", np.float32, 1)]
+    timed = _timed_variants(one_job, seconds_budget, variants)
+    job_bytes = TOKENS * CHANNELS * 2  # the bf16 slot a job writes
+    rates = {label: {"value": round(units * job_bytes / seconds / 1e9, 4), "jobs": units,
+                     "seconds": round(seconds, 2)} for label, (units, seconds) in timed.items()}
+    return {"value": rates["fp64_all_threads"]["value"], "unit": "GB/s", "cores": cores, "kind": "port",
+            "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(), "variants": rates,
+            "sample": "CausVid restore jobs (one chunk's K or V: 4680 x 1536 bf16 slot, r 128 with Wan RoPE / 192) "
+                      "through oracle.restore (dequantize, numpy product, RoPE, bf16 cast); value = the reference's "
+                      f"default FP64 on all {cores} host threads; FP32 and 1-thread variants beside it"}
 
 
 # ---------------------------------------------------------------------------------------------
@@ -232,37 +288,62 @@ def fit_step(sources, contexts, device):
 
 
 def fit_cpu_baseline(seconds_budget=20.0, seed=3):
-    """The oracle's CPU restatement of the fit chain per matrix (FP32 Gram, LAPACK eigh, crossing,
-    FP64-accumulated projection, 8-bit quantization) on a bounded sample of CausVid-shape matrices."""
+    """The oracle's CPU restatement of the fit chain per matrix (Gram, LAPACK eigh, crossing,
+    FP64-accumulated projection, 8-bit quantization), the Gram and eigh in FP32 (the method's
+    arithmetic) or FP64, with all host threads and with one BLAS thread, on CausVid-shape
+    matrices generated before the timing."""
     from oracle import fit as of
     from oracle import quantize as oq
 
     rng = np.random.default_rng(seed)
-    threads = os.cpu_count() or 1
-    matrices = 0
-    started = time.perf_counter()
-    generation = 0.0
-    while True:
-        began = time.perf_counter()
-        x = of.to_bfloat16_values(of.decaying_spectrum(rng, TOKENS, CHANNELS))
-        generation += time.perf_counter() - began
-        gram = x.T @ x  # FP32 product (BLAS threads)
-        values, vectors = np.linalg.eigh(gram)
+    cores = host_threads()
+    sources = [of.to_bfloat16_values(of.decaying_spectrum(rng, TOKENS, CHANNELS)) for _ in range(2)]
+    cursor = [0]
+
+    def one_matrix(compute):
+        x = sources[cursor[0] % len(sources)]
+        target = 0.98 if cursor[0] % 2 == 0 else 0.95
+        cursor[0] += 1
+        operand = x.astype(compute)
+        values, vectors = np.linalg.eigh(operand.T @ operand)
         values, rows = values[::-1], vectors[:, ::-1].T
         total = float(np.square(x.astype(np.float64)).sum())
-        rank = of.bucket(of.crossing(values.astype(np.float64), total, 0.98 if matrices % 2 == 0 else 0.95), 32,
-                         CHANNELS)
-        stored = of.stored_basis(rows[:rank])
-        oq.quantize(of.project(x, stored), "per_channel")
-        matrices += 1
-        elapsed = time.perf_counter() - started - generation
-        if elapsed >= seconds_budget or matrices >= 8:
-            break
-    per_matrix = elapsed / matrices
-    return {"value": round(1.0 / (per_matrix * 2 * LAYERS), 4), "unit": "chunks/s", "cores": threads, "kind": "port",
-            "sample": f"{matrices} CausVid-shape matrices [4680, 1536] through oracle.fit (numpy FP32 Gram, LAPACK "
-                      f"eigh, crossing, FP64 projection, quantizer) on {threads} host threads; "
-                      f"{per_matrix * 1e3:.0f} ms/matrix, 60 matrices per chunk"}
+        rank = of.bucket(of.crossing(values.astype(np.float64), total, target), 32, CHANNELS)
+        oq.quantize(of.project(x, of.stored_basis(rows[:rank])), "per_channel")
+
+    variants = [("fp32_all_threads", np.float32, cores), ("fp64_all_threads", np.float64, cores),
+                ("fp32_1_thread", np.float32, 1), ("fp64_1_thread", np.float64, 1)]
+    timed = _timed_variants(one_matrix, seconds_budget, variants)
+    rates = {label: {"value": round(units / seconds / (2 * LAYERS), 5), "matrices": units,
+                     "ms_per_matrix": round(seconds / units * 1e3, 1)} for label, (units, seconds) in timed.items()}
+    return {"value": rates["fp32_all_threads"]["value"], "unit": "chunks/s", "cores": cores, "kind": "port",
+            "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(), "variants": rates,
+            "sample": "CausVid-shape matrices [4680, 1536] (60 per chunk) through oracle.fit: Gram + LAPACK eigh "
+                      "(FP32 as the method computes them, or FP64), crossing, FP64 projection, quantizer; value = "
+                      f"FP32 on all {cores} host threads; FP64 and 1-thread variants beside it"}
+
+
+def fit_kernel_probe(device, rank=32):
+    """One launch each of the fit chunk's batched device kernels at its shape (60 sources [4680,
+    1536] bf16; rank-32 orthonormal bases from a host QR): absmax, Gram, projection, residual
+    energies.  Values do not matter to the counters; no eigensolver or QR runs on the device."""
+    from reelcache_amd import fit_kernels as fk
+
+    generator = torch.Generator(device=device).manual_seed(9)
+    rng = np.random.default_rng(9)
+    count = 2 * LAYERS
+    sources = [torch.randn(TOKENS, CHANNELS, device=device, generator=generator).to(torch.bfloat16)
+               for _ in range(count)]
+    basis = torch.from_numpy(np.linalg.qr(rng.standard_normal((CHANNELS, rank)))[0].T.copy()).to(device)
+    bases, ranks = [basis.to(torch.float16)] * count, [rank] * count
+    torch.cuda.synchronize(device)
+    keys = fk.absmax(sources)
+    fk.gram(sources)
+    coefficients, _ = fk.project(sources, bases, ranks, extrema=True)
+    fk.energies(sources, keys, bases=bases, ranks=ranks, coefficients=coefficients)
+    torch.cuda.synchronize(device)
+    return {"sources": count, "shape": [TOKENS, CHANNELS], "rank": rank,
+            "kernels": "absmax, gram, project (with column extrema), energies (source and residual)"}
 
 
 def fit_leg(device, steps, warmup, cpu_seconds):
@@ -347,8 +428,9 @@ def longcat_leg(device, layers, reps):
         jobs = []
         for _target in range(2):
             cache = torch.empty((1, LC_HEADS, history, HEAD_DIM), dtype=torch.bfloat16, device=device)
-            gauss = torch.randn(channels, LC_MAX_RANK, device=device, generator=generator, dtype=torch.float32)
-            basis = torch.linalg.qr(gauss).Q.T.contiguous().to(torch.bfloat16)
+            # Orthonormal rows: host QR of a seeded Gaussian (float64), stored as the bf16 basis.
+            gauss = rng.standard_normal((channels, LC_MAX_RANK))
+            basis = torch.from_numpy(np.linalg.qr(gauss)[0].T.copy()).to(device=device, dtype=torch.bfloat16)
             for chunk in range(LC_CHUNKS):
                 rank = int(rng.integers(8, 17)) * 32
                 codes = torch.randint(0, 256, (TOKENS, rank), dtype=torch.uint8, device=device, generator=generator)
@@ -569,6 +651,10 @@ def main():
                         help="skip the step timed in the single-product fp16 precision mode")
     parser.add_argument("--pictures-layers", type=int, default=4,
                         help="layers restored from picture canvases beside the headline (0 skips the leg)")
+    parser.add_argument("--fit-kernel-probe", action="store_true",
+                        help="run the fit chunk's device kernels once each on 60 seeded Gaussian sources (absmax, "
+                             "Gram, projection, residual energies) without the planner: the dispatches counter "
+                             "passes summarize")
     parser.add_argument("--copy-probe", action="store_true",
                         help="after the timed region, run 3 plain device copies of 256 MiB (the calibration "
                              "dispatches for rocprofv3 FETCH_SIZE / WRITE_SIZE passes)")
@@ -653,11 +739,26 @@ def main():
     written, algorithmic = layer_bytes()
     value = LAYERS * written / (ms_per_step / 1e3) / 1e9
     kernel_avg = float(np.mean(kernel_ms))
-    # The restore launches' own duration: the sum of the intervals between the events recorded
-    # after the pack and after each restore launch (the event after the last launch and the
-    # call's closing event are not kernel time).
-    launches_avg = float(np.mean([sum(durations) for durations in launch_ms]))
-    achieved = algorithmic / (launches_avg / 1e3) / 1e9
+    # Live per-launch durations (HIP events on the launch stream around each launch of the
+    # stage-event step): K, then V; the pack before them.
+    k_us, v_us = (float(v) * 1e3 for v in np.mean(np.array(launch_ms), axis=0)[:2])
+    pack_us = float(np.mean(pack_ms)) * 1e3
+    profile = profile_figures()
+    pack_bytes = 2 * (RANK_K + RANK_V) * CHANNELS * 2
+    split = {}
+    for name, rank, us in (("K", RANK_K, k_us), ("V", RANK_V, v_us), ("pack", None, pack_us)):
+        nbytes = launch_bytes(rank) if rank else pack_bytes
+        entry = {"us": round(us, 2), "algorithmic_bytes": nbytes, "achieved_gbs": round(nbytes / us / 1e3, 1),
+                 "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+        if f"traffic_bytes_per_launch {name}" in profile:
+            entry["traffic"] = int(profile[f"traffic_bytes_per_launch {name}"])
+            entry["rocprof_us"] = profile[f"trace_us {name}"]
+        if f"mfma_busy {name}" in profile:
+            entry["mfma_busy"] = profile[f"mfma_busy {name}"]
+        split[name] = entry
+    dominant = split["V"]
+    launches_avg = (k_us + v_us) / 1e3
+    achieved = dominant["achieved_gbs"]
     result = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
@@ -677,15 +778,21 @@ def main():
                   "host_us_per_layer_call": round(enqueued / LAYERS * 1e6, 1),
                   "what": "median of 3 eager steps (30 reconstruct calls each, no graph, no stage events): "
                           "host planning + enqueue overlapped with the device"},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "traffic_source": "profiles/restore_causvid_traffic.md (rocprofv3 FETCH_SIZE + WRITE_SIZE per "
-                                       "layer call, calibrated on a 256 MiB copy)",
-                     "kernel": "restore_fast_kernel, the K and V launches of a layer call (" + ", ".join(variants) +
-                               "); the basis pack before them is reported as pack_us and in layer_gpu",
-                     "algorithmic_bytes_per_layer_call": algorithmic,
-                     "launches_us": round(launches_avg * 1e3, 2),
-                     "mfma_tflops": round(2 * layer_flops() / (launches_avg / 1e3) / 1e12, 1)},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": dominant.get("traffic"),
+                     "kernel": "restore_fast_kernel<4, 12, false, 2, 2, 1>: the V launch of a layer call (7 jobs, "
+                               "rank 192), the longest of the call's launches",
+                     "algorithmic_bytes_per_launch": dominant["algorithmic_bytes"],
+                     "launch_us": dominant["us"],
+                     "traffic_source": "profiles/restore_causvid_counters.md (rocprofv3 FETCH_SIZE + WRITE_SIZE per "
+                                       "dispatch, calibrated on 256 MiB copies)",
+                     "split": split,
+                     "layer_call": {"launches_us": round(launches_avg * 1e3, 2),
+                                    "algorithmic_bytes": algorithmic,
+                                    "achieved_gbs": round(algorithmic / (launches_avg / 1e3) / 1e9, 1),
+                                    "traffic": int(profile["traffic_bytes_per_layer_call"])
+                                    if "traffic_bytes_per_layer_call" in profile else None,
+                                    "mfma_tflops": round(2 * layer_flops() / (launches_avg / 1e3) / 1e12, 1)}},
         "layer_gpu": {"us": round(float(np.mean(layer_ms)) * 1e3, 2),
                       "achieved_gbs": round(algorithmic / (float(np.mean(layer_ms)) / 1e3) / 1e9, 1),
                       "what": "one eager layer call on the device, first launch (basis pack) to last restore launch "
@@ -714,6 +821,8 @@ def main():
     if args.fit_steps > 0:
         result.update(fit_leg(device, args.fit_steps, args.fit_warmup,
                               0.0 if args.no_cpu_baseline else args.cpu_seconds))
+    if args.fit_kernel_probe:
+        result["fit_kernel_probe"] = fit_kernel_probe(device)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(result), flush=True)
