@@ -52,7 +52,8 @@ def bound(value: Any, name: str) -> float | None:
 
 
 def host_floats(value: Any, length: int, name: str) -> np.ndarray:
-    """A contiguous finite float32 host vector of ``length`` entries (a host tensor is copied)."""
+    """A read-only finite float32 host copy of a vector of ``length`` entries (the caller's array
+    can change afterwards without changing what the holder of the copy reads)."""
     if isinstance(value, torch.Tensor):
         need(value.device.type == "cpu", f"{name} must be a host array; pass the packet affine payload")
         value = value.detach().numpy()
@@ -60,7 +61,9 @@ def host_floats(value: Any, length: int, name: str) -> np.ndarray:
     need(array.dtype == np.float32 and array.shape == (length,),
          f"{name} must be a float32 vector with one entry per rank column")
     need(np.isfinite(array).all(), f"{name} must be finite")
-    return np.ascontiguousarray(array)
+    copy = np.array(array, dtype=np.float32, copy=True, order="C")
+    copy.flags.writeable = False
+    return copy
 
 
 def one_of(value: Any, choices: tuple, name: str) -> Any:

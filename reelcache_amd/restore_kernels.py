@@ -57,7 +57,7 @@ from .restore_model import (COEFFICIENT_DTYPES, LAYOUTS, OUTPUT_DTYPES, Coeffici
                             PictureSource, ReconstructionJob, RopePositions, RopeTable, expand_affine, wan_sections)
 from .restore_plan import (DEFAULT_MERGED, _DEFAULT_CONFIG, _RETIRED_SLABS, _STAGING, BASIS_DTYPES, SLICE_JOBS,  # noqa: F401
                            SLICE_TOKENS, STREAM_TOKENS, TILE_TOKENS, _balanced_bounds, _capture_staging,
-                           _coefficient_bound, _coefficient_bounds, _fast_flags, _pinned_bytes, _prescale_exponent,
+                           _coefficient_bound, _fast_flags, _pinned_bytes, _prescale_exponent,
                            _slice_heads, _slice_plan, _tiles, job_desc, reserve_capture_staging, run_call)
 from .restore_reference import (_OUTPUT_FLOOR, _UNIT_ROUNDOFF, _check_compute_dtype,  # noqa: F401
                                 _check_disjoint, _facts, _gemm_gamma, _native_rotation, _require_fp32_matmul, _storage_key,

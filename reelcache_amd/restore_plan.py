@@ -79,24 +79,9 @@ def _prescale_exponent(bound):
     return max(-100, min(100, 14 - ceiling))
 
 
-def _prescale_exponents(bounds):
-    """:func:`_prescale_exponent` of many bounds at once (same float32 rounding and clamp)."""
-    bounds = np.asarray(bounds, dtype=np.float32).astype(np.float64)
-    mantissa, exponent = np.frexp(bounds)
-    ceiling = exponent - (mantissa == 0.5)
-    return np.where(bounds > 0, np.clip(14 - ceiling, -100, 100), 0).astype(np.int64)
-
-
 def _coefficient_bound(scale, offset):
     """Upper bound of ``|pixel * scale + offset|`` over 8-bit pixels (reelcache/restore_kernels.py:1782-1785)."""
     return float(max(np.abs(offset).max(), np.abs(np.float32(255) * scale + offset).max())) * 1.0001
-
-
-def _coefficient_bounds(scales, offsets, starts):
-    """:func:`_coefficient_bound` of consecutive segments ``[starts[i], starts[i + 1])`` of
-    concatenated fp32 affine vectors, in one vectorized pass (same fp32 arithmetic)."""
-    magnitude = np.maximum(np.abs(offsets), np.abs(np.float32(255) * scales + offsets))
-    return np.maximum.reduceat(magnitude, starts).astype(np.float64) * 1.0001
 
 
 _STAGING_LOCK = threading.Lock()
@@ -381,9 +366,9 @@ class _JobDesc:
     of a call's geometry key.  Addresses (destination, source, basis, tables) are read from the
     referenced tensors at every call."""
 
-    __slots__ = ("basis", "basis_key", "channels", "dst", "dst_shift", "dst_vec_rule", "dtype", "grid", "head_dim",
-                 "host_bound", "key", "kind", "offset", "out_dtype", "pictures", "rank", "rope_kind", "row", "scale",
-                 "section_pairs", "src", "src_vec_rule", "table", "tokens")
+    __slots__ = ("affine", "basis", "basis_key", "channels", "dst", "dst_shift", "dst_vec_rule", "dtype",
+                 "exponent", "grid", "head_dim", "host_bound", "key", "key_id", "kind", "out_dtype", "pictures",
+                 "rank", "rope_kind", "row", "section_pairs", "src", "src_vec_rule", "table", "tokens")
 
     def __init__(self, job):
         view, source = job.destination, job.source
@@ -398,8 +383,8 @@ class _JobDesc:
         self._rope(row, job)
         self.kind, dtype = _source_kind(job)
         self.dtype = _DTYPE_CODES[dtype]
-        self.src = self.pictures = self.basis = self.basis_key = self.scale = self.offset = self.host_bound = None
-        self.src_vec_rule, self.rank = False, 0
+        self.src = self.pictures = self.basis = self.basis_key = self.affine = self.host_bound = None
+        self.src_vec_rule, self.rank, self.exponent = False, 0, 0
         if isinstance(source, DenseSource):
             self.src = source.values
             row[_C_SRC_DTYPE] = self.dtype
@@ -410,6 +395,7 @@ class _JobDesc:
         pictures = None if self.pictures is None else (len(source.pictures), len(source.pictures[0]))
         self.key = (row.tobytes(), self.kind, self.dtype, self.out_dtype, self.head_dim, self.channels, self.rope_kind,
                     self.basis_key, self.host_bound is None, pictures, self.section_pairs)
+        self.key_id = _KEY_IDS.setdefault(self.key, len(_KEY_IDS))
 
     def _destination(self, row, view, tensor):
         size = tensor.element_size()
@@ -461,21 +447,31 @@ class _JobDesc:
             row[_C_PIC_SLOTS], row[_C_PIC_PLANES] = layout["channels_per_segment"], layout["planes"]
             row[_C_PIC_COLS] = layout["grid"][0]
             row[_C_PIC_PLANE_STRIDE], row[_C_PIC_ROW_STRIDE] = source.plane_stride, source.row_stride
-            self.scale, self.offset = source.scale, source.offset
+            self._affine(source.scale, source.offset)
             return
         values = self.src = source.values
         row[_C_SRC_DTYPE] = self.dtype
         row[_C_SRC_ROW], row[_C_SRC_COL] = values.stride()
         if source.quantized:
-            self.scale, self.offset = source.scale[:self.rank], source.offset[:self.rank]
+            self._affine(source.scale[:self.rank], source.offset[:self.rank])
             self.src_vec_rule = values.stride(1) == 1 and values.stride(0) % 16 == 0
         else:
             self.host_bound = source.bound
+
+    def _affine(self, scale, offset):
+        """The job's fp32 (scale | offset) block and the fp16 modes' prescale exponent of its
+        coefficient bound max(|offset|, |255 * scale + offset|) (the affine arrays are read-only copies)."""
+        self.affine = np.concatenate((scale, offset)).astype(np.float32, copy=False)
+        self.exponent = _prescale_exponent(_coefficient_bound(scale, offset))
 
     def source_address(self):
         if self.pictures is None:
             return self.src.data_ptr()
         return min(picture.data_ptr() for picture in self.pictures)
+
+
+# Distinct job geometries (descriptor keys) seen by this process, numbered for cheap call keys.
+_KEY_IDS: dict = {}
 
 
 def job_desc(job):
@@ -574,19 +570,19 @@ class _Layout:
         self.host_bound_jobs = [i for i, d in enumerate(descs) if self.fp16_mode and d.host_bound is not None]
 
     def _affine_layout(self, descs, rows, relative, arena):
-        """One fp32 (scale | offset) table for every job with an affine; its offsets in the rows."""
-        self.affine_jobs = [i for i, d in enumerate(descs) if d.scale is not None]
-        ranks = [descs[i].rank for i in self.affine_jobs]
-        self.affine_starts = np.concatenate(([0], np.cumsum(ranks)[:-1])).astype(np.int64) if ranks else None
-        self.affine_total = int(sum(ranks))
-        self.affine_offset = arena.reserve(8 * self.affine_total) if ranks else None
+        """One fp32 table of every job's (scale | offset) block, in job order; the rows' pointers."""
+        self.affine_jobs = [i for i, d in enumerate(descs) if d.affine is not None]
+        sizes = [descs[i].affine.size for i in self.affine_jobs]
+        self.affine_total = int(sum(sizes))
+        self.affine_offset = arena.reserve(4 * self.affine_total) if sizes else None
         self.affine_at = {}
-        for position, index in enumerate(self.affine_jobs):
-            first = int(self.affine_starts[position])
-            at = (self.affine_offset + 4 * first, self.affine_offset + 4 * (self.affine_total + first))
+        first = 0
+        for index, size in zip(self.affine_jobs, sizes):
+            at = (self.affine_offset + 4 * first, self.affine_offset + 4 * (first + size // 2))
             self.affine_at[index] = at
             rows[index, _C_SCALE], rows[index, _C_OFFSET] = at
             relative[index, _C_SCALE] = relative[index, _C_OFFSET] = 1
+            first += size
 
     def _launch_groups(self, descs, rows, arena, device):
         """Launch groups (source kind, dtypes, head geometry, rank class, straight-line eligibility)
@@ -801,15 +797,10 @@ class _Layout:
         image = host.numpy()
         image[:] = self.template
         if self.affine_jobs:
-            scales = np.concatenate([descs[index].scale for index in self.affine_jobs])
-            offsets = np.concatenate([descs[index].offset for index in self.affine_jobs])
-            table = image[self.affine_offset:self.affine_offset + 8 * self.affine_total].view(np.float32)
-            table[:self.affine_total], table[self.affine_total:] = scales, offsets
+            image[self.affine_offset:self.affine_offset + 4 * self.affine_total].view(np.float32)[:] = \
+                np.concatenate([descs[index].affine for index in self.affine_jobs])
             if self.fp16_mode:
-                # The fp16 modes' prescale: bound max(|offset|, |255 * scale + offset|) of every job in
-                # one vectorized pass, then its power-of-two exponent.
-                bounds = _coefficient_bounds(scales, offsets, self.affine_starts)
-                rows[self.affine_jobs, _C_COEF_EXP] = _prescale_exponents(bounds)
+                rows[self.affine_jobs, _C_COEF_EXP] = [descs[index].exponent for index in self.affine_jobs]
         for index in self.host_bound_jobs:
             rows[index, _C_COEF_EXP] = _prescale_exponent(descs[index].host_bound)
         for index, at in self.picture_tables:
@@ -908,7 +899,7 @@ def run_call(descs, device, stream, precision, config, keepalive, stage_events=N
         if desc.basis is not None:
             bases[index] = address = desc.basis.data_ptr()
             groups[index] = first_of.setdefault((address, desc.basis_key), index)
-    key = (precision, _config_key(config), tuple(desc.key for desc in descs), tuple(dynamic), tuple(groups))
+    key = (precision, _config_key(config), tuple(desc.key_id for desc in descs), tuple(dynamic), tuple(groups))
     layout = _LAYOUTS.get(key)
     if layout is None:
         layout = _Layout(descs, dynamic, groups, precision, config, device)

@@ -146,7 +146,7 @@ def unpack_pictures(source):
 def dequantize(pixels, scale, offset):
     """``float(pixel) * scale + offset`` rounded twice: the product, then the sum (no fused
     multiply-add), as the eager reference computes it."""
-    scale_t, offset_t = (torch.as_tensor(np.ascontiguousarray(v), device=pixels.device) for v in (scale, offset))
+    scale_t, offset_t = (torch.tensor(np.asarray(v, dtype=np.float32), device=pixels.device) for v in (scale, offset))
     product = pixels.to(torch.float32) * scale_t
     return product + offset_t
 

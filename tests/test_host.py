@@ -256,18 +256,6 @@ def test_fast_eligibility_rules():
     assert rk._fast_flags(row, odd, "fp16x2") == 0  # head_dim % 32 != 0
 
 
-def test_vectorized_coefficient_bounds_match_the_per_job_rule():
-    rng = np.random.default_rng(28)
-    ranks = [128, 192, 1, 77, 300]
-    scales = [rng.uniform(0, 3, size=r).astype(np.float32) for r in ranks]
-    offsets = [rng.uniform(-500, 500, size=r).astype(np.float32) for r in ranks]
-    starts = np.concatenate(([0], np.cumsum(ranks)[:-1]))
-    bounds = rk._coefficient_bounds(np.concatenate(scales), np.concatenate(offsets), starts)
-    for bound, scale, offset in zip(bounds, scales, offsets):
-        assert float(bound) == rk._coefficient_bound(scale, offset)
-        assert rk._prescale_exponent(float(bound)) == rk._prescale_exponent(rk._coefficient_bound(scale, offset))
-
-
 def test_captured_calls_need_reserved_staging(monkeypatch):
     monkeypatch.setattr(rp, "_STAGING", {})
     with pytest.raises(ConfigurationError, match="reserve_capture_staging"):
@@ -300,10 +288,3 @@ def test_replaced_staging_slab_stays_alive(monkeypatch):
     unused = rp._STAGING["slab"][0]
     rp.reserve_capture_staging(1 << 21)
     assert not any(kept is unused for kept in rp._RETIRED_SLABS)
-
-
-def test_vectorized_prescale_exponents_match_the_scalar_rule():
-    rng = np.random.default_rng(29)
-    bounds = np.concatenate([[0.0, -1.0, 2.0 ** -140, 1.0, 0.5, 2.0 ** 13, 2.0 ** 14, 3.0e38, 1e-45, 16383.999],
-                             rng.lognormal(0, 20, size=2000)])
-    np.testing.assert_array_equal(rp._prescale_exponents(bounds), [rk._prescale_exponent(b) for b in bounds])
