@@ -101,6 +101,20 @@ class ModelIdentity:
         else:
             _count(self.kv_channels, "kv_channels")
 
+    def to_dict(self) -> dict[str, Any]:
+        """JSON form (the field names of the reference's record)."""
+        def plain(value):
+            return dict(value) if isinstance(value, Mapping) else value
+        return {"name": self.name, "fingerprint": self.fingerprint, "layers": self.layers,
+                "kv_channels": plain(self.kv_channels), "layout": self.layout, "dtype": plain(self.dtype)}
+
+    @classmethod
+    def from_dict(cls, data: Mapping[str, Any]) -> "ModelIdentity":
+        try:
+            return cls(**dict(data))
+        except (TypeError, KeyError) as error:
+            raise ConfigurationError("invalid model identity fields") from error
+
     def channels_for(self, target) -> int:
         target = target.target if isinstance(target, MatrixKey) else target
         if target not in _TARGETS:
@@ -136,6 +150,12 @@ class MatrixKey:
     def to_dict(self) -> dict[str, Any]:
         return {"layer": self.layer, "target": self.target}
 
+    @classmethod
+    def from_dict(cls, data: Mapping[str, Any]) -> "MatrixKey":
+        if not isinstance(data, Mapping) or set(data) != {"layer", "target"}:
+            raise ConfigurationError("a matrix key is {layer, target}")
+        return cls(data["layer"], data["target"])
+
 
 @dataclass(frozen=True)
 class TensorContext:
@@ -164,6 +184,24 @@ class TensorContext:
             raise ConfigurationError("V matrices must use key_space='none'")
         if self.source_dtype is not None:
             object.__setattr__(self, "source_dtype", canonical_dtype(self.source_dtype))
+
+    def to_dict(self) -> dict[str, Any]:
+        """JSON form (the field names of the reference's record; ``source_dtype`` only when set)."""
+        record = {"model": self.model.to_dict(), "key": self.key.to_dict(), "token_start": self.token_start,
+                  "frames": self.frames, "height": self.height, "width": self.width, "key_space": self.key_space}
+        if self.source_dtype is not None:
+            record["source_dtype"] = self.source_dtype
+        return record
+
+    @classmethod
+    def from_dict(cls, data: Mapping[str, Any]) -> "TensorContext":
+        try:
+            fields = dict(data)
+            fields["model"] = ModelIdentity.from_dict(fields["model"])
+            fields["key"] = MatrixKey.from_dict(fields["key"])
+            return cls(**fields)
+        except (TypeError, KeyError) as error:
+            raise ConfigurationError("invalid tensor context fields") from error
 
     @property
     def channels(self) -> int:
@@ -294,3 +332,41 @@ def energy_targets(profile: str) -> EnergyTargets:
 
 __all__ = ["CodecSpec", "ENERGY_TARGET_PROFILES", "EnergyTargets", "MatrixKey", "ModelIdentity", "RANK_BUCKET",
            "TensorContext", "canonical_digest", "canonical_dtype", "energy_targets"]
+
+
+def json_copy(value: Any, *, name: str = "metadata") -> Any:
+    """A deep copy of a JSON value (dicts, lists, strings, finite numbers, booleans, None); anything
+    else is a ConfigurationError naming ``name``."""
+    try:
+        return json.loads(json.dumps(value, allow_nan=False))
+    except (TypeError, ValueError) as error:
+        raise ConfigurationError(f"{name} must be JSON data") from error
+
+
+@dataclass(frozen=True)
+class EncodedTensor:
+    """An encoded packet: JSON ``metadata``, named byte ``payloads``, optionally the FP16 ``basis``
+    bytes of a single-matrix packet and JSON ``metrics`` (reelcache/types.py:349-371)."""
+
+    metadata: Mapping[str, Any]
+    payloads: Mapping[str, bytes]
+    basis: bytes | None = None
+    metrics: Mapping[str, Any] | None = None
+
+    def __post_init__(self) -> None:
+        if not isinstance(self.metadata, Mapping) or not isinstance(self.payloads, Mapping):
+            raise ConfigurationError("encoded metadata and payloads must be mappings")
+        if not self.payloads:
+            raise ConfigurationError("encoded tensors require at least one payload")
+        for name, payload in self.payloads.items():
+            _nonempty(name, "payload name")
+            if not isinstance(payload, bytes):
+                raise ConfigurationError("encoded payloads must be immutable bytes")
+        if self.basis is not None and not isinstance(self.basis, bytes):
+            raise ConfigurationError("encoded basis must be immutable bytes")
+        if self.metrics is not None and not isinstance(self.metrics, Mapping):
+            raise ConfigurationError("metrics must be a mapping")
+        object.__setattr__(self, "metadata", json_copy(self.metadata))
+        object.__setattr__(self, "payloads", MappingProxyType(dict(self.payloads)))
+        if self.metrics is not None:
+            object.__setattr__(self, "metrics", json_copy(self.metrics, name="metrics"))

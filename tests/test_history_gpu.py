@@ -6,6 +6,10 @@ and a fork v1b = v0 + 16..64 rows; ranks are ragged in [64, min(256, version row
 32-grid.  The nodes are gathered in a seeded random fork order through the device basis cache
 (one resident tip per chain, ancestors served as prefixes) and restored with one call per layer.
 
+The versions come either from the in-memory chain (``BasisVersions``) or from a
+``BasisVersionStore`` (content-addressed FP16 row blocks and version manifests, the stored
+format), read by the device basis cache through the same interface.
+
 Gather / indexing is checked bit for bit: the caches equal those of the same restore given
 explicit bases built from the test's own rows of each version (not from the cache's views).
 Values of one node per version (v0, v1, the v2 tip and the v1b fork) are checked against the
@@ -19,7 +23,9 @@ import torch
 
 from oracle import restore as orc
 from reelcache_amd import archive_restore as ar
+from reelcache_amd import basis_versions as bv
 from reelcache_amd import restore_kernels as rk
+from reelcache_amd.types import MatrixKey, ModelIdentity
 
 from restore_cases import random_affine
 
@@ -29,10 +35,16 @@ HEADS, HEAD_DIM, GRID = 12, 128, (3, 30, 52)
 TOKENS, CHANNELS = 4680, 1536
 
 
-def _versions(rng, layers):
-    """The product's version store and the test's own rows of every version (root first)."""
-    versions = ar.BasisVersions()
-    own = {}
+def _versions(rng, layers, source="memory"):
+    """The product's version source and the test's own rows of every version (root first);
+    versions are named by their references (``{layer}{target}:{name}`` in memory, manifest
+    references in the store)."""
+    if source == "memory":
+        versions = ar.BasisVersions()
+    else:
+        model = ModelIdentity("causvid-history", "a" * 64, layers, CHANNELS, "THD", "bfloat16")
+        versions = bv.BasisVersionStore(bv.MemoryObjectStore(), model)
+    own, names = {}, {}
     for layer in range(layers):
         for target in ("K", "V"):
             sizes = {"v0": 192, "v1": int(rng.integers(16, 65)), "v2": int(rng.integers(16, 65)),
@@ -43,9 +55,16 @@ def _versions(rng, layers):
             rows = torch.from_numpy(q.T.copy()).to(torch.float16)
             start, spans = 0, {}
             for name in ("v0", "v1", "v2", "v1b"):
-                ref = f"{layer}{target}:{name}"
-                parent = None if parents[name] is None else f"{layer}{target}:{parents[name]}"
-                versions.add(ref, parent, rows[start:start + sizes[name]])
+                block = rows[start:start + sizes[name]]
+                parent = None if parents[name] is None else names[f"{layer}{target}:{parents[name]}"]
+                if source == "memory":
+                    ref = f"{layer}{target}:{name}"
+                    versions.add(ref, parent, block)
+                elif parent is None:
+                    ref, _ = versions.put_root(MatrixKey(layer, target), block)
+                else:
+                    ref, _ = versions.put_extension(parent, block)
+                names[f"{layer}{target}:{name}"] = ref
                 spans[name] = (start, start + sizes[name])
                 start += sizes[name]
             for name in ("v0", "v1", "v2", "v1b"):
@@ -53,8 +72,8 @@ def _versions(rng, layers):
                 while walk is not None:
                     chain.append(spans[walk])
                     walk = parents[walk]
-                own[f"{layer}{target}:{name}"] = torch.cat([rows[a:b] for a, b in reversed(chain)], 0)
-    return versions, own
+                own[names[f"{layer}{target}:{name}"]] = torch.cat([rows[a:b] for a, b in reversed(chain)], 0)
+    return versions, own, names
 
 
 def _rank(rng, total):
@@ -63,17 +82,18 @@ def _rank(rng, total):
     return int(rng.choice(grid)) if rng.random() < 0.7 else int(rng.integers(64, high + 1))
 
 
-def test_fork_history_gather_is_exact(device):
+@pytest.mark.parametrize("source", ["memory", "store"])
+def test_fork_history_gather_is_exact(device, source):
     rng = np.random.default_rng(60)
     layers = 2
-    versions, own = _versions(rng, layers)
+    versions, own, refs = _versions(rng, layers, source)
     names = ["v0"] * 3 + ["v1"] * 3 + ["v2"] * 3 + ["v1b"] * 3
     nodes = []
     for index, name in enumerate(names):
         matrices = {}
         for layer in range(layers):
             for target in ("K", "V"):
-                ref = f"{layer}{target}:{name}"
+                ref = refs[f"{layer}{target}:{name}"]
                 rank = _rank(rng, versions.total_rank(ref))
                 codes = torch.randint(0, 256, (TOKENS, rank), dtype=torch.uint8,
                                       generator=torch.Generator().manual_seed(int(rng.integers(1 << 30))))
