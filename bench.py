@@ -261,8 +261,8 @@ def fit_workload(device, seed=2, distinct=60):
 
 
 def fit_step(sources, contexts, device):
-    """One chunk: plan every matrix, then project onto its planned rows and quantize (device)."""
-    from reelcache_amd import fit_kernels as fk
+    """One chunk: plan every matrix, then finalize it on its planned rows (projection, stored and
+    span energies, codes; device)."""
     from reelcache_amd import gpu_fitting as gf
     from reelcache_amd import node_packets as npk
     from reelcache_amd import rank_method as rm
@@ -276,14 +276,18 @@ def fit_step(sources, contexts, device):
         chunk_id="bench", source_ids={k: str(k) for k in keys})
     torch.cuda.synchronize(device)
     planned = time.perf_counter()
-    rows = [plan.plans[k].new_rows.to(device) for k in keys]
-    ranks = [int(r.shape[0]) for r in rows]
-    coefficients, extrema = fk.project([sources[k] for k in keys], rows, ranks, extrema=True)
-    host_keys = extrema.cpu().numpy()
-    codes = [pixels for pixels, _, _ in npk.quantize_many(coefficients, host_keys,
-                                                         [config.spec_for(r) for r in ranks])]
+    # Final measurement on the planned FP16 rank views: projection, stored and span energies,
+    # condition bound and 8-bit codes of all 60 matrices in batched launches.
+    items = []
+    for k in keys:
+        matrix_plan = plan.plans[k]
+        rows = matrix_plan.new_rows.to(device)
+        items.append(npk.FinalizeItem(sources[k], rows, contexts[k], config.spec_for(int(rows.shape[0])), k,
+                                      matrix_plan.target, False, matrix_plan.new_rows))
+    finalized = npk.finalize_tiles(items, tile_rows=config.tile_rows)
+    codes = [pixels for _, pixels in finalized]
     torch.cuda.synchronize(device)
-    plan.stages["finalize"] = time.perf_counter() - planned  # projection onto the planned rows + quantization
+    plan.stages["finalize"] = time.perf_counter() - planned  # finalize_tiles of the chunk
     return plan, codes
 
 

@@ -12,6 +12,9 @@ Restates, in float64 numpy, what the reference computes on its fitting path:
   fp32 rounding of the FP64 dot product of the exact operands;
 * :func:`energies` -- the FP64 source and direct residual energies scaled by max|X|
   (reelcache/factorization.py:398-419, :692-724);
+* :func:`span_energy` -- the ideal energy of the stored rows' span, ``||L^-1 P^T||_F^2 / ||X||^2``
+  with ``L L^T = Q Q^T`` in FP64 (reelcache/deferred_reads.py:682-714, the value
+  ``reelcache/node_packets.py:370-371`` records as a tile's ideal energy);
 * :func:`crossing` / :func:`bucket` -- DirectionSet.crossing (reelcache/rank_method.py:411-417)
   and _bucket (:487-490);
 * :func:`decaying_spectrum` -- the synthetic fit workload (sigma_i = i ** -1.2 plus noise);
@@ -19,7 +22,8 @@ Restates, in float64 numpy, what the reference computes on its fitting path:
 
 How each is pinned (tests/test_oracle_fit.py): brute-force Python sums on tiny inputs, SVD
 subspaces, exact rational arithmetic for the projection, closed forms for the energies of
-coordinate bases, and hand-counted crossings.
+coordinate bases (and, for the span energy, of any invertible mix of coordinate rows: the span
+is unchanged), and hand-counted crossings.
 """
 
 from __future__ import annotations
@@ -78,6 +82,18 @@ def energies(x, basis16=None, coefficients=None, rank: int | None = None) -> tup
     if scale:
         x, error = x / scale, error / scale
     return scale, float(np.square(x).sum()), float(np.square(error).sum())
+
+
+def span_energy(coefficients, basis16, source_energy: float) -> float:
+    """Share of the source energy in the span of the stored rows: ``||L^-1 P^T||_F^2 / E`` where
+    ``L`` is the Cholesky factor of the FP64 Gram ``Q Q^T`` of the FP16 rows and ``P`` the fp32
+    coefficients (1 for a zero source; ValueError for singular rows)."""
+    if source_energy <= 0:
+        return 1.0
+    q = np.asarray(basis16, dtype=np.float16).astype(np.float64)
+    factor = np.linalg.cholesky(q @ q.T)
+    solved = np.linalg.solve(factor, as_float(coefficients).T)  # lower-triangular system
+    return float(np.square(solved).sum() / source_energy)
 
 
 def crossing(energies_desc, total: float, fraction: float) -> int | None:

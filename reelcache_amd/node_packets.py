@@ -276,3 +276,12 @@ def pack_tile_index(metadata: Mapping[str, Any]) -> dict[Any, int]:
         key = MatrixKey.from_dict(tile["key"])
         index[key if tile["stream"] is None else (key, tile["stream"])] = position
     return index
+
+
+# Final measurement and node canvases live in :mod:`reelcache_amd.finalize` (they use the functions
+# above); the reference's module exports them from here.
+from .finalize import (FinalizeItem, FinalTile, NodeCanvas, assemble_canvas, finalize_tile,  # noqa: E402
+                       finalize_tiles, pack_codec)
+
+__all__ += ["FinalTile", "FinalizeItem", "NodeCanvas", "assemble_canvas", "finalize_tile", "finalize_tiles",
+            "pack_codec"]

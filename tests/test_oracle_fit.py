@@ -111,3 +111,23 @@ def test_bfloat16_rounding_matches_torch():
     x[:4] = [1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -(1.0 + 2 ** -8), 0.0]  # ties to even
     expected = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
     np.testing.assert_array_equal(of.to_bfloat16_values(x), expected)
+
+
+def test_span_energy_closed_forms():
+    """Coordinate rows e_i: the span energy is the energy of those columns of X (P = X[:, idx]).
+    Any invertible mix A of the same rows spans the same subspace, so the value does not change
+    (a dropped Gram inverse fails this); an orthonormal complement adds the rest (total 1)."""
+    rng = np.random.default_rng(41)
+    x = rng.integers(-8, 9, size=(50, 8)).astype(np.float64)  # small integers: every P below is exact in fp32
+    total = float(np.square(x).sum())
+    idx = [1, 4, 6]
+    coordinate = np.eye(8)[idx].astype(np.float16)
+    p = of.project(x, coordinate)
+    expected = float(np.square(x[:, idx]).sum()) / total
+    assert abs(of.span_energy(p, coordinate, total) - expected) <= 1e-12
+    mix = np.array([[2.0, 0.0, 0.0], [0.5, 1.0, 0.0], [-1.0, 0.25, 4.0]])  # exact in fp16 products
+    mixed = (mix @ coordinate.astype(np.float64)).astype(np.float16)
+    assert abs(of.span_energy(of.project(x, mixed), mixed, total) - expected) <= 1e-12
+    everything = np.eye(8).astype(np.float16)
+    assert abs(of.span_energy(of.project(x, everything), everything, total) - 1.0) <= 1e-12
+    assert of.span_energy(np.zeros((50, 3)), coordinate, 0.0) == 1.0
