@@ -6,7 +6,7 @@
   FP64 condition bound, below 1.5 for rounded orthonormal bases, and the exact bound for a
   basis that is not near orthonormal (tests/test_gpu_fitting_batched.py:64-77);
 * the oracle's ``coefficient_bound`` (reelcache/restore_kernels.py:1782-1785) against a
-  brute-force maximum over all 256 codes, and the product's vectorized bound against it.
+  brute-force maximum over all 256 codes, and the product's per-job bound against it.
 """
 
 import math
