@@ -55,3 +55,48 @@ def test_longcat_shape_restore(device):
         got = got[torch.from_numpy(rows).to(got.device)].reshape(len(rows), -1).double().cpu().numpy()
         excess = np.abs(got - values) - bound
         assert float(excess.max()) <= 0, f"{int((excess > 0).sum())} elements exceed the error bound"
+
+
+@pytest.mark.parametrize("precision", ["fp16x2", "fp16"])
+def test_longcat_shape_beside_a_concurrent_gemm(device, precision):
+    """The LongCat layer restored while 4096 x 4096 bf16 GEMMs run on a second stream (the next
+    chunk's forward) gives the same bits as the restore alone, within the precision's bound; the
+    single-product fp16 mode takes the one-wave kernel at 16 rank steps and rank halves above."""
+    rng = np.random.default_rng(92)
+    tokens = int(np.prod(GRID))
+    history = len(RANKS) * tokens
+    cases, caches = [], []
+    for target in range(2):
+        cache = destination("BHTD", history, HEADS, HEAD_DIM, "bfloat16", device, fill=FILL)
+        basis = orthonormal_basis(512, HEADS * HEAD_DIM, rng, torch.bfloat16).to(device)
+        caches.append(cache)
+        for chunk, rank in enumerate(RANKS):
+            view = rk.NativeView(cache, "BHTD", token_offset=chunk * tokens)
+            cases.append(make_case(rng, grid=GRID, heads=HEADS, head_dim=HEAD_DIM, rank=rank, rope="none",
+                                   view=view, basis=basis, out_dtype="bfloat16", device=device))
+    jobs = [case.job for case in cases]
+    handle = rk.reconstruct(jobs, precision=precision)
+    handle.release()
+    expected = {"fp16x2": {"split"}, "fp16": {"split", "fast"}}[precision]
+    assert set(handle.stats["variants"]) == expected, handle.stats["variants"]
+    alone = [cache.clone() for cache in caches]
+    for cache in caches:
+        cache.fill_(FILL)
+    a = torch.randn(4096, 4096, device=device, dtype=torch.bfloat16)
+    b = torch.randn(4096, 4096, device=device, dtype=torch.bfloat16)
+    side, main = torch.cuda.Stream(device), torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    main.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        products = [a @ b for _ in range(6)]
+    rk.reconstruct(jobs, precision=precision, stream=main).release()
+    torch.cuda.synchronize(device)
+    del products
+    for cache, reference in zip(caches, alone):
+        assert torch.equal(cache, reference), "the restore beside a GEMM differs from the restore alone"
+    for case in cases:
+        rows = np.unique(np.concatenate(([0, tokens - 1], rng.choice(tokens, 16, replace=False))))
+        values, bound = orc.error_bound(case.coefficients[rows], case.basis, HEADS, None, precision, "bfloat16")
+        got = case.job.destination.slot(tokens)
+        got = got[torch.from_numpy(rows).to(got.device)].reshape(len(rows), -1).double().cpu().numpy()
+        assert float((np.abs(got - values) - bound).max()) <= 0
