@@ -222,10 +222,10 @@ def _config(**kwargs):
 def test_planner_config_and_binding_rules():
     assert _config().solver_id() == "fp32_gram_topk_rr.v1:m64:s3"  # the reference's default solver
     assert _config(solver="gram_eigh").solver_id() == "fp32_gram_eigh.v1"
-    with pytest.raises(UnsupportedError):
-        _config(solver="warm_start")
-    with pytest.raises(UnsupportedError):
-        _config(refit_rule="cumulative")
+    assert _config(solver="warm_start").solver_id(warm=True) == "fp32_gram_warm_rr.v1:s1"
+    assert _config(refit_rule="cumulative").refit_rule == "cumulative"
+    with pytest.raises(ConfigurationError):
+        _config(solver="power")
     with pytest.raises(ConfigurationError):
         _config(decision_band=0.1)
     with pytest.raises(ConfigurationError):
