@@ -358,7 +358,8 @@ def fit_leg(device, steps, warmup, cpu_seconds):
     for _ in range(warmup):
         fit_step(sources, contexts, device)
         print("fit: warmup chunk done", file=sys.stderr, flush=True)
-    stages = {"energy": 0.0, "gram": 0.0, "topk": 0.0, "eigh": 0.0, "verify": 0.0, "finalize": 0.0}
+    stages = {"energy": 0.0, "gram": 0.0, "sketch": 0.0, "predict": 0.0, "topk": 0.0, "eigh": 0.0, "verify": 0.0,
+              "finalize": 0.0}
     torch.cuda.synchronize(device)
     began = time.perf_counter()
     plan = None

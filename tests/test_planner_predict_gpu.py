@@ -230,3 +230,34 @@ def test_refit_from_the_parent_basis(device, solver):
     assert label <= plan.observed_rank <= label + 32 and plan.bucket_rank >= -(-label // 32) * 32
     assert plan.decision_energy == pytest.approx(_stored_energy(host, plan.new_rows.numpy()), abs=1e-9)
     assert plan.decision_energy >= 0.98 + 1e-6
+
+
+def test_bounded_working_set_plans_in_groups(device):
+    """``max_working_bytes`` splits the chunk into consecutive groups whose planning tensors fit
+    half the budget (reelcache/rank_method.py:1152-1168); the decisions and verified ranks equal the
+    unbounded plan's."""
+    rng = np.random.default_rng(76)
+    model = ModelIdentity("bounded-test", "6" * 64, 2, 512, "THD", "bfloat16")
+    sigma = np.arange(1, 513, dtype=np.float64) ** -0.9
+    sources, contexts = {}, {}
+    for layer, target in ((0, "K"), (0, "V"), (1, "K"), (1, "V")):
+        key = MatrixKey(layer, target)
+        sources[key] = _spectrum(rng, 2000, 512, sigma)[0]
+        contexts[key] = _context(model, key, 2000)
+    config = _config(0.98)
+    keys = list(sources)
+    bindings = {key: rm.ActiveBasisBinding() for key in keys}
+    parents = {key: None for key in keys}
+    ids = {k: f"s{k.layer}{k.target}" for k in keys}
+    whole = rm.GramPlanner(config, device=device).plan({k: sources[k].to(device) for k in keys}, contexts, bindings,
+                                                       parents, chunk_id="c1", source_ids=ids)
+    per_matrix = 3 * 4 * 2000 * 512 + 3 * 4 * 512 * 512 + 3 * 8 * 1024 * 512
+    bounded = rm.GramPlanner(config, device=device, max_working_bytes=2 * (2 * per_matrix)).plan(
+        {k: sources[k].to(device) for k in keys}, contexts, bindings, parents, chunk_id="c1", source_ids=ids)
+    assert whole.memory is None
+    assert bounded.memory["group_size"] == 2 and bounded.memory["groups"] == 2
+    assert bounded.memory["matrix_bytes_estimate"] == per_matrix
+    for key in keys:
+        a, b = whole.plans[key], bounded.plans[key]
+        assert (a.decision, a.bucket_rank) == (b.decision, b.bucket_rank)
+        assert b.decision_energy == pytest.approx(a.decision_energy, abs=1e-6)
