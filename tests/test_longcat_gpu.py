@@ -3,7 +3,7 @@ LongCat's [B, H, T, D] cache layout, 4680-token chunks with high per-chunk ranks
 512-row bf16 basis per K/V target), no RoPE (LongCat stores pre-RoPE K,
 reelcache/restore_kernels.py:504-506).
 
-Three chunks per target keep the oracle affordable; the checks are
+Two tests restore three chunks per target, one the full 16-chunk history; the checks are
   * every element of every slot is written (no fill value left) and the tokens around the slots
     are untouched;
   * sampled token rows of every job against the oracle's elementwise error bound
@@ -97,6 +97,39 @@ def test_longcat_shape_beside_a_concurrent_gemm(device, precision):
     for case in cases:
         rows = np.unique(np.concatenate(([0, tokens - 1], rng.choice(tokens, 16, replace=False))))
         values, bound = orc.error_bound(case.coefficients[rows], case.basis, HEADS, None, precision, "bfloat16")
+        got = case.job.destination.slot(tokens)
+        got = got[torch.from_numpy(rows).to(got.device)].reshape(len(rows), -1).double().cpu().numpy()
+        assert float((np.abs(got - values) - bound).max()) <= 0
+
+
+def test_longcat_full_history(device):
+    """The full configs[4] history of one layer: 16 chunks per target with ranks drawn from the
+    32-grid in [256, 512], restored in one call; every slot written, the tokens around untouched,
+    sampled rows of every job within the oracle's bound."""
+    rng = np.random.default_rng(93)
+    chunks = 16
+    tokens = int(np.prod(GRID))
+    history = chunks * tokens
+    cases, caches = [], []
+    for target in range(2):
+        cache = destination("BHTD", history, HEADS, HEAD_DIM, "bfloat16", device, offset=3, extra=3, fill=FILL)
+        basis = orthonormal_basis(512, HEADS * HEAD_DIM, rng, torch.bfloat16).to(device)
+        caches.append(cache)
+        ranks = rng.choice(np.arange(256, 513, 32), size=chunks)
+        for chunk, rank in enumerate(ranks):
+            view = rk.NativeView(cache, "BHTD", token_offset=3 + chunk * tokens)
+            cases.append(make_case(rng, grid=GRID, heads=HEADS, head_dim=HEAD_DIM, rank=int(rank), rope="none",
+                                   view=view, basis=basis, out_dtype="bfloat16", device=device))
+    handle = rk.reconstruct([case.job for case in cases])
+    handle.release()
+    assert set(handle.stats["variants"]) == {"split"}, handle.stats["variants"]
+    for cache in caches:
+        tokens_major = cache[0].transpose(0, 1)
+        assert not bool((tokens_major[3:3 + history] == FILL).any()), "a slot element was not written"
+        assert bool((tokens_major[:3] == FILL).all()) and bool((tokens_major[3 + history:] == FILL).all())
+    for case in cases:
+        rows = np.unique(np.concatenate(([0, tokens - 1], rng.choice(tokens, 12, replace=False))))
+        values, bound = orc.error_bound(case.coefficients[rows], case.basis, HEADS, None, "fp16x2", "bfloat16")
         got = case.job.destination.slot(tokens)
         got = got[torch.from_numpy(rows).to(got.device)].reshape(len(rows), -1).double().cpu().numpy()
         assert float((np.abs(got - values) - bound).max()) <= 0
