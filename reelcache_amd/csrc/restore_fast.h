@@ -217,10 +217,14 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
             constexpr int kGroups = kRanks / 16;
             constexpr int kIters = (kTileTokens * kGroups + kThreadsT - 1) / kThreadsT;
             const __amdgpu_buffer_rsrc_t src = make_rsrc(J->src_ptr + t0 * rs, (tokens - t0) * rs);
+            // Rank halves: the thread index made opaque here, so the staging offsets are
+            // recomputed per tile instead of being hoisted out of the tile loop (and spilled).
+            int me = tid;
+            if constexpr (SPLIT == 2) asm volatile("" : "+v"(me));
             u4 bytes[kIters];
 #pragma unroll
             for (int i = 0; i < kIters; ++i) {
-                const int q = tid + i * kThreadsT;
+                const int q = me + i * kThreadsT;
                 const int token = q / kGroups, g = q - token * kGroups;
                 const uint32_t offset = (q < kTileTokens * kGroups && 16 * g < rank)
                                             ? static_cast<uint32_t>(token * rs + 16 * g)
@@ -229,7 +233,7 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
             }
 #pragma unroll
             for (int i = 0; i < kIters; ++i) {
-                const int q = tid + i * kThreadsT;
+                const int q = me + i * kThreadsT;
                 const int token = q / kGroups, g = q - token * kGroups;
                 if (q < kTileTokens * kGroups) {
                     // Bytes past the rank (row padding) are staged as they are: their affine
@@ -305,7 +309,10 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
         const uint8_t* mine = codes + (group * 32 + col) * kPitch;
 #pragma unroll
         for (int s = 0; s < kKsWave; ++s) {
-            const int kl = 16 * (half * kKsWave + s) + 8 * h;
+            int kl = 16 * (half * kKsWave + s) + 8 * h;
+            // Rank halves hold 12-16 fragments per wave: a step's LDS reads wait for the previous
+            // step's fragment (ordered asm statements), or the hoisted reads of later steps spill.
+            if constexpr (SPLIT == 2) asm volatile("" : "+v"(kl));
             const u2 b = *reinterpret_cast<const u2*>(mine + kl);
             const f4 sc0 = *reinterpret_cast<const f4*>(affine + kl);
             const f4 sc1 = *reinterpret_cast<const f4*>(affine + kl + 4);
@@ -320,6 +327,7 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
                 a[j + 4] = dequant((b[1] >> (8 * j)) & 0xffu, sc1[j], of1[j]);
             }
             set_frag_scaled(cf[s], a);
+            if constexpr (SPLIT == 2) asm volatile("" ::"v"(cf[s].hi));
         }
         if constexpr (SPLIT == 2) __syncthreads();  // codes are read; the steps reuse them for partial sums
     };
