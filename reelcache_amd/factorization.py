@@ -128,8 +128,9 @@ def validate_stored_basis(basis: torch.Tensor, channels: int) -> torch.Tensor:
 
 
 def _canonical_signs(basis: torch.Tensor) -> torch.Tensor:
-    """Rows flipped so that the first entry of largest magnitude of each row is positive."""
-    pivot = basis.gather(1, basis.abs().argmax(dim=1, keepdim=True))
+    """Rows flipped so that the first entry of largest magnitude of each row is positive; a
+    ``[..., rows, C]`` batch is handled in one reduction (rows along the last dimension)."""
+    pivot = basis.gather(-1, basis.abs().argmax(dim=-1, keepdim=True))
     return basis * torch.where(pivot < 0, -1.0, 1.0).to(basis.dtype)
 
 
