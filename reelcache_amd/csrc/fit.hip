@@ -388,12 +388,15 @@ __global__ void __launch_bounds__(kThreads) project_kernel(const rch_fit_matrix*
 }
 
 // ---------------------------------------------------------------------------------------------
-// Residual energies on v_mfma_f64_16x16x4f64: D[m = channel][n = token] = sum_k Q[k][c] P[token][k].
+// Residual energies on v_mfma_f64_16x16x4f64: D[m = token][n = channel] = sum_k P[token][k] Q[k][c].
 // Workgroup = 64-token tile of one matrix, wave w = tokens 16w .. 16w + 15, looping over
-// 16-channel blocks.  Per 16-rank step a lane (i = l % 16, g = l / 16) loads P[token i][4g .. 4g + 3]
-// (one 16-byte load) and Q[4g .. 4g + 3][channel i]; MFMA step j takes rank 4g + j.
-// The f64 accumulator holds element v of lane l at row (l / 16) + 4v, column l % 16: channel
-// g + 4v of the block and token i, compared with X[token][channel].
+// 64-channel groups.  A group is four 16 x 16 blocks whose columns interleave: column i of
+// block b is channel 4i + b of the group, so after the four blocks lane l (i = l % 16,
+// g = l / 16) holds channels 4i .. 4i + 3 of tokens g + 4v (v = 0..3, the f64 accumulator's row
+// (l / 16) + 4v): X and the residual move as 4-channel vectors, 16 lanes covering 64 contiguous
+// channels of a row.  Per 16-rank step a lane loads P[token i][4g .. 4g + 3] (one 16-byte load,
+// the A operand; MFMA step j takes rank 4g + j) and, for each j, Q[4g + j][4i .. 4i + 3] (one
+// 8-byte load: the B operands of the four blocks).
 // ---------------------------------------------------------------------------------------------
 
 template <int DT>
@@ -415,47 +418,65 @@ __global__ void __launch_bounds__(kThreads) residual_kernel(const rch_fit_matrix
     const float smax = __uint_as_float(*gin<unsigned int>(M->absmax_ptr));
     const double s = static_cast<double>(smax);
     const bool scaled = smax != 0.0f;
-    const uint32_t x_row = static_cast<uint32_t>(i16 * M->src_stride * E);
     const uint32_t p_row = static_cast<uint32_t>(i16 * M->coef_stride * 4);
-    const bool t_ok = wt + i16 < rows;
-    RCH_GLOBAL float* resid = M->resid_ptr ? gout<float>(M->resid_ptr) + (wt + i16) * channels : nullptr;
+    const uint32_t q_stride = static_cast<uint32_t>(M->basis_stride * 2);
+    RCH_GLOBAL float* resid = M->resid_ptr ? gout<float>(M->resid_ptr) : nullptr;
 
     double src = 0.0, err = 0.0;
-    for (int cb = 0; cb < channels; cb += 16) {
-        d4 acc = d4{};
+    for (int c64 = 0; c64 < channels; c64 += 64) {
+        const int c = c64 + 4 * i16;  // this lane's 4 channels (channels % 8 == 0: all or none in range)
+        const bool c_ok = c < channels;
+        d4 acc[4] = {d4{}, d4{}, d4{}, d4{}};
         for (int k0 = 0; k0 < rank; k0 += 16) {
             const int k = k0 + 4 * g;
             const u4 pw = __builtin_amdgcn_raw_buffer_load_b128(ps, k < rank ? p_row + static_cast<uint32_t>(k * 4) : kOutOfRange,
                                                                 0, 0);
-            double qa[4], pb[4];
+            u2 qw[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const bool in = k + j < rank;  // P rows may hold padding beyond the rank
-                pb[j] = in ? static_cast<double>(__uint_as_float(pw[j])) : 0.0;
-                const uint32_t q_off = (in && cb + i16 < channels)
-                                           ? static_cast<uint32_t>(((k + j) * M->basis_stride + cb + i16) * 2)
-                                           : kOutOfRange;
-                const uint32_t qb = __builtin_amdgcn_raw_buffer_load_b16(qs, q_off, 0, 0);
-                qa[j] = static_cast<double>(half_bits<RCH_DT_F16>(qb));
+                const uint32_t q_off = (k + j < rank && c_ok) ? static_cast<uint32_t>(k + j) * q_stride + 2u * c : kOutOfRange;
+                qw[j] = __builtin_amdgcn_raw_buffer_load_b64(qs, q_off, 0, 0);
             }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f64_16x16x4f64(qa[j], pb[j], acc, 0, 0, 0);
+            for (int j = 0; j < 4; ++j) {
+                // P rows may hold padding beyond the rank; its basis rows read as zero.
+                const double pa = k + j < rank ? static_cast<double>(__uint_as_float(pw[j])) : 0.0;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const uint32_t half = (qw[j][b >> 1] >> (16 * (b & 1))) & 0xffffu;
+                    const double qb = static_cast<double>(half_bits<RCH_DT_F16>(half));
+                    acc[b] = __builtin_amdgcn_mfma_f64_16x16x4f64(pa, qb, acc[b], 0, 0, 0);
+                }
+            }
         }
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            const int c = cb + g + 4 * v;
-            const uint32_t offset = c < channels ? x_row + static_cast<uint32_t>(c * E) : kOutOfRange;
-            double a;
-            if constexpr (DT == RCH_DT_F32)
-                a = static_cast<double>(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xs, offset, 0, 0)));
-            else
-                a = static_cast<double>(half_bits<DT>(__builtin_amdgcn_raw_buffer_load_b16(xs, offset, 0, 0)));
-            const double e = a - acc[v];
-            if (resid && c < channels && t_ok) resid[c] = static_cast<float>(e);
-            // The scale s is applied once per tile below: sum (a / s)^2 = (sum a^2) / s^2 up to
-            // the rounding of the FP64 sums (relative 1e-16), without two FP64 divisions per element.
-            src += a * a;
-            err += e * e;
+            const int token = g + 4 * v;
+            const uint32_t offset = c_ok ? static_cast<uint32_t>((token * M->src_stride + c) * E) : kOutOfRange;
+            double a[4];
+            if constexpr (DT == RCH_DT_F32) {
+                const u4 w = __builtin_amdgcn_raw_buffer_load_b128(xs, offset, 0, 0);
+#pragma unroll
+                for (int b = 0; b < 4; ++b) a[b] = static_cast<double>(__uint_as_float(w[b]));
+            } else {
+                const u2 w = __builtin_amdgcn_raw_buffer_load_b64(xs, offset, 0, 0);
+#pragma unroll
+                for (int b = 0; b < 4; ++b) a[b] = static_cast<double>(half_bits<DT>((w[b >> 1] >> (16 * (b & 1))) & 0xffffu));
+            }
+            double e[4];
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                e[b] = a[b] - acc[b][v];
+                // The scale s is applied once per tile below: sum (a / s)^2 = (sum a^2) / s^2 up to
+                // the rounding of the FP64 sums (relative 1e-16), without two FP64 divisions per element.
+                src += a[b] * a[b];
+                err += e[b] * e[b];
+            }
+            if (resid && c_ok && token < left) {
+                const f4 out = {static_cast<float>(e[0]), static_cast<float>(e[1]), static_cast<float>(e[2]),
+                                static_cast<float>(e[3])};
+                *reinterpret_cast<RCH_GLOBAL f4*>(resid + (wt + token) * channels + c) = out;
+            }
         }
     }
     // Fixed-order reduction: butterfly within the wave, then waves 0..3 in order.
