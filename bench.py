@@ -278,12 +278,17 @@ def fit_step(sources, contexts, device):
     planned = time.perf_counter()
     # Final measurement on the planned FP16 rank views: projection, stored and span energies,
     # condition bound and 8-bit codes of all 60 matrices in batched launches.
-    items = []
-    for k in keys:
+    # The planned rows (host, one block per matrix) go to the device in one pinned transfer.
+    host_rows = [plan.plans[k].new_rows for k in keys]
+    staged = torch.cat([rows.reshape(-1) for rows in host_rows]).pin_memory()
+    device_rows = staged.to(device, non_blocking=True)
+    items, offset = [], 0
+    for k, host in zip(keys, host_rows):
         matrix_plan = plan.plans[k]
-        rows = matrix_plan.new_rows.to(device)
+        rows = device_rows[offset:offset + host.numel()].view(host.shape)
+        offset += host.numel()
         items.append(npk.FinalizeItem(sources[k], rows, contexts[k], config.spec_for(int(rows.shape[0])), k,
-                                      matrix_plan.target, False, matrix_plan.new_rows))
+                                      matrix_plan.target, False, host))
     finalized = npk.finalize_tiles(items, tile_rows=config.tile_rows)
     codes = [pixels for _, pixels in finalized]
     torch.cuda.synchronize(device)

@@ -397,6 +397,18 @@ typedef struct rch_quantize_job {
  */
 int rch_quantize_batched(const rch_quantize_job* jobs_dev, int n_jobs, int64_t max_rows, void* stream);
 
+/*
+ * Batched upper Cholesky factor and its inverse, in FP64: for each of n symmetric positive
+ * definite k x k matrices A (row-major, contiguous, only the upper triangle read), R upper with
+ * A = R^T R and x = R^{-1} (upper, zeros below).  info[b] = 0, or j + 1 when the leading minor of
+ * order j + 1 is not positive definite (LAPACK's convention), x[b] is then the identity.
+ * 1 <= k <= RCH_CHOLESKY_MAX_K (one workgroup per matrix, the matrix in LDS).
+ * Replaces the torch.linalg.cholesky_ex + trsm_right_upper pair of each CholeskyQR step
+ * (reelcache/rank_method.py:738-752, :676-685).
+ */
+#define RCH_CHOLESKY_MAX_K 128
+int rch_cholesky_inverse(const double* a_dev, double* x_dev, int32_t* info_dev, int n, int k, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -87,6 +87,7 @@ _SIGNATURES = {
     "rch_column_extrema": ([_p, _i64, _i, _i64, _p, _p], _i),
     "rch_quantize": ([_p, _i64, _i, _i64, _p, _p, _p, _i64, _p], _i),
     "rch_quantize_batched": ([_p, _i, _i64, _p], _i),
+    "rch_cholesky_inverse": ([_p, _p, _p, _i, _i, _p], _i),
 }
 # Further entry points registered by other modules are bound when present.
 _OPTIONAL_SIGNATURES: dict = {}

@@ -581,6 +581,78 @@ __global__ void __launch_bounds__(kThreads) quantize_batched_kernel(const rch_qu
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Batched FP64 Cholesky factor and triangular inverse (the planner's CholeskyQR steps): one
+// workgroup per k x k matrix held row-major in LDS.  Right-looking factorization, one column per
+// step: the pivot row is scaled by 1 / sqrt(pivot) (one reciprocal, kept for the solve), then
+// the trailing upper triangle takes the rank-1 update.  The inverse X = R^-1 is solved row by row from the bottom (lane c owns column
+// c): row i of R is copied aside, then X[i][c] = -(sum_{p > i} R[i][p] X[p][c]) / R[i][i] overwrites
+// R[i][c] -- every lane reads the same R[i][p] and neighbouring X[p][c], so LDS reads do not
+// conflict, and rows below i of R are no longer needed.
+// ---------------------------------------------------------------------------------------------
+
+constexpr int kCholThreads = 512;
+
+__global__ void __launch_bounds__(kCholThreads) cholesky_inverse_kernel(const double* __restrict__ a,
+                                                                         double* __restrict__ x,
+                                                                         int32_t* __restrict__ info, int k) {
+    __shared__ double m[RCH_CHOLESKY_MAX_K * RCH_CHOLESKY_MAX_K];
+    __shared__ double diag[RCH_CHOLESKY_MAX_K], row[RCH_CHOLESKY_MAX_K];
+    const int tid = threadIdx.x;
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * k * k;
+    const RCH_GLOBAL double* A = gin<double>(reinterpret_cast<int64_t>(a)) + base;
+    RCH_GLOBAL double* X = gout<double>(reinterpret_cast<int64_t>(x)) + base;
+    for (int e = tid; e < k * k; e += kCholThreads) m[e] = A[e];
+    __syncthreads();
+    int failed = 0;
+    for (int j = 0; j < k; ++j) {
+        const double d = m[j * k + j];  // every thread reads the same pivot: the branch is uniform
+        if (!(d > 0.0) || !(d < INFINITY)) {
+            failed = j + 1;
+            break;
+        }
+        const double r = sqrt(d), inv = 1.0 / r;
+        for (int c = j + 1 + tid; c < k; c += kCholThreads) m[j * k + c] *= inv;
+        __syncthreads();
+        if (tid == 0) diag[j] = inv;  // the reciprocal of R[j][j]
+        // Trailing upper triangle: lanes over columns (the pivot row's entry of the column in a
+        // register), waves over rows; the rows of a lane are independent updates.
+        for (int c = j + 1 + (tid & 63); c < k; c += 64) {
+            const double q = m[j * k + c];
+#pragma unroll 4
+            for (int i = j + 1 + (tid >> 6); i <= c; i += kCholThreads / 64) m[i * k + c] -= m[j * k + i] * q;
+        }
+        __syncthreads();
+    }
+    if (failed) {
+        for (int i = tid >> 6; i < k; i += kCholThreads / 64)
+            for (int c = tid & 63; c < k; c += 64) X[i * k + c] = i == c ? 1.0 : 0.0;
+        if (tid == 0) info[blockIdx.x] = failed;
+        return;
+    }
+    for (int i = k - 1; i >= 0; --i) {
+        for (int c = i + 1 + tid; c < k; c += kCholThreads) row[c] = m[i * k + c];
+        __syncthreads();
+        for (int c = i + tid; c < k; c += kCholThreads) {
+            // Four partial sums keep four LDS reads in flight.
+            double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+            int p = i + 1;
+            for (; p + 3 <= c; p += 4) {
+                s0 += row[p] * m[p * k + c];
+                s1 += row[p + 1] * m[(p + 1) * k + c];
+                s2 += row[p + 2] * m[(p + 2) * k + c];
+                s3 += row[p + 3] * m[(p + 3) * k + c];
+            }
+            for (; p <= c; ++p) s0 += row[p] * m[p * k + c];
+            m[i * k + c] = ((c == i ? 1.0 : 0.0) - ((s0 + s1) + (s2 + s3))) * diag[i];
+        }
+        __syncthreads();
+    }
+    for (int i = tid >> 6; i < k; i += kCholThreads / 64)
+        for (int c = tid & 63; c < k; c += 64) X[i * k + c] = i <= c ? m[i * k + c] : 0.0;
+    if (tid == 0) info[blockIdx.x] = 0;
+}
+
 int check_matrices(const rch_fit_matrix* mats, int n, int channels, const char* what) {
     if (!mats || n <= 0 || n > 65535) return fail(RCH_E_CONFIG, "%s: 1 <= n_mats <= 65535 required", what);
     if (channels <= 0 || channels % 8 != 0 || channels > (1 << 20))
@@ -668,6 +740,14 @@ int rch_quantize(const float* values_dev, int64_t rows, int cols, int64_t stride
     hipLaunchKernelGGL(quantize_kernel, dim3(static_cast<unsigned>((rows + 63) / 64)), dim3(kThreads), 0,
                        as_stream(stream), values_dev, rows, cols, stride, scale_dev, offset_dev, codes_dev, code_stride);
     return check_launch("rch_quantize");
+}
+
+int rch_cholesky_inverse(const double* a_dev, double* x_dev, int32_t* info_dev, int n, int k, void* stream) {
+    if (!a_dev || !x_dev || !info_dev || n <= 0 || k <= 0 || k > RCH_CHOLESKY_MAX_K)
+        return fail(RCH_E_CONFIG, "rch_cholesky_inverse: 1 <= k <= %d and device buffers required", RCH_CHOLESKY_MAX_K);
+    hipLaunchKernelGGL(cholesky_inverse_kernel, dim3(static_cast<unsigned>(n)), dim3(kCholThreads), 0, as_stream(stream),
+                       a_dev, x_dev, info_dev, k);
+    return check_launch("rch_cholesky_inverse");
 }
 
 int rch_quantize_batched(const rch_quantize_job* jobs_dev, int n_jobs, int64_t max_rows, void* stream) {

@@ -75,7 +75,11 @@ def _table(count: int) -> np.ndarray:
 
 
 def _upload(table: np.ndarray, device: torch.device) -> torch.Tensor:
-    return torch.from_numpy(table.view(np.int64).copy()).to(device)
+    """The descriptor table on the device, copied from pinned memory on the current stream without
+    a host wait (a pageable copy would drain the stream first).  The pinned block stays reserved
+    until the copy has run (torch's host allocator records it on the stream)."""
+    staged = torch.from_numpy(table.view(np.int64)).pin_memory()
+    return staged.to(device, non_blocking=True)
 
 
 def _fill_sources(table: np.ndarray, sources) -> None:
@@ -232,6 +236,25 @@ def energies(sources, absmax_keys: torch.Tensor, *, bases=None, ranks=None, coef
               _DTYPE_CODES[aligned[0].dtype], _stream(device))
     del keep
     return (totals, outputs) if residuals else totals
+
+
+CHOLESKY_MAX_K = 128  # RCH_CHOLESKY_MAX_K: one k x k FP64 matrix per workgroup, held in LDS
+
+
+def cholesky_inverse(gram: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(inverse, info)`` of a batch ``[n, k, k]`` of FP64 symmetric positive definite matrices on
+    the device (k <= :data:`CHOLESKY_MAX_K`): ``inverse = R^-1`` with ``A = R^T R`` (R upper, only
+    the upper triangle of A read) and int32 ``info`` (0, or j + 1 when the leading minor of order
+    j + 1 is not positive definite; that member's inverse is the identity), in one launch."""
+    if (gram.ndim != 3 or gram.shape[1] != gram.shape[2] or gram.dtype != torch.float64
+            or gram.device.type != "cuda" or not 1 <= gram.shape[1] <= CHOLESKY_MAX_K or gram.shape[0] < 1):
+        raise ConfigurationError(f"cholesky_inverse takes a device float64 [n, k, k] batch with k <= {CHOLESKY_MAX_K}")
+    a = gram.contiguous()
+    inverse = torch.empty_like(a)
+    info = torch.empty(a.shape[0], dtype=torch.int32, device=a.device)
+    _lib.call("rch_cholesky_inverse", a.data_ptr(), inverse.data_ptr(), info.data_ptr(), int(a.shape[0]),
+              int(a.shape[1]), _stream(a.device))
+    return inverse, info
 
 
 def column_extrema(values: torch.Tensor) -> torch.Tensor:

@@ -7,6 +7,8 @@
   per-column extrema are exactly the min / max of the returned coefficients.
 * energies: FP64, relative 1e-12 of the oracle.
 * quantizer: codes bit-exact with the oracle on the same coefficients and affine.
+* Cholesky factor and inverse (CholeskyQR): relative 1e-12 of numpy's FP64 factorization;
+  LAPACK's info convention for indefinite members.
 """
 
 import functools
@@ -177,3 +179,45 @@ def test_batched_quantizer_matches_single_launches(device):
         single = fk.quantize(v, torch.from_numpy(affine[0].copy()).to(device), torch.from_numpy(affine[1].copy()).to(device))
         np.testing.assert_array_equal(codes.cpu().numpy(), single.cpu().numpy())
         np.testing.assert_array_equal(codes.cpu().numpy(), oq.quantize_with_affine(v.cpu().numpy(), affine[0], affine[1]))
+
+
+@pytest.mark.parametrize("k", [1, 7, 96, 128])
+def test_cholesky_inverse_matches_fp64_factorization(device, k):
+    """The batched factor-and-inverse launch of the planner's CholeskyQR steps against numpy's
+    FP64 Cholesky (A = R^T R, R = L^T) and the exact triangular inverse: relative 1e-12 on
+    well-conditioned matrices; R^-1 R = I; the lower triangle is zero."""
+    from scipy.linalg import solve_triangular
+
+    rng = np.random.default_rng(31 + k)
+    batch = []
+    for _ in range(5):
+        q, _ = np.linalg.qr(rng.standard_normal((k, k)))
+        batch.append((q * rng.uniform(1.0, 30.0, k)) @ q.T)  # condition <= 900
+    a = np.stack(batch)
+    inverse, info = fk.cholesky_inverse(torch.from_numpy(a).to(device))
+    inverse, info = inverse.cpu().numpy(), info.cpu().numpy()
+    assert (info == 0).all()
+    for member, got in zip(a, inverse):
+        r = np.linalg.cholesky(member).T
+        want = solve_triangular(r, np.eye(k), lower=False)
+        assert np.abs(got - want).max() <= 1e-12 * np.abs(want).max()
+        assert np.abs(got @ r - np.eye(k)).max() <= 1e-12
+        assert (np.tril(got, -1) == 0).all()
+
+
+def test_cholesky_inverse_flags_indefinite_members(device):
+    """LAPACK's info convention: j + 1 for the first leading minor that is not positive definite
+    (a negative pivot at order 4, a NaN at order 1); such members come back as the identity and
+    do not disturb the others."""
+    k = 6
+    good = np.diag(np.arange(1.0, k + 1.0))
+    indefinite = np.diag([1.0, 2.0, 3.0, -1.0, 5.0, 6.0])
+    nan = good.copy()
+    nan[0, 0] = np.nan
+    inverse, info = fk.cholesky_inverse(torch.from_numpy(np.stack([good, indefinite, nan])).to(device))
+    assert info.cpu().tolist() == [0, 4, 1]
+    inverse = inverse.cpu().numpy()
+    np.testing.assert_allclose(inverse[0], np.diag(1.0 / np.sqrt(np.arange(1.0, k + 1.0))), rtol=1e-15)
+    assert (inverse[1] == np.eye(k)).all() and (inverse[2] == np.eye(k)).all()
+    with pytest.raises(Exception):
+        fk.cholesky_inverse(torch.zeros((1, 129, 129), dtype=torch.float64, device=device))
