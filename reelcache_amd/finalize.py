@@ -246,6 +246,7 @@ def finalize_tiles(items: Sequence[FinalizeItem], *, tile_rows: int, keep_coeffi
         values, scalars = _measure_group([items[i] for i in members], [ranks[i] for i in members])
         for position, index in enumerate(members):
             coefficients[index], measured[index] = values[position], scalars[position]
+    _, _, finite = fit_kernels.split_keys_many(np.stack([m["extrema"] for m in measured]), ranks)
     tiles = []
     for index, (item, rank, m) in enumerate(zip(items, ranks, measured)):
         need(m["bits"] < fit_kernels.NONFINITE_BITS, "projection requires a nonempty finite FP32-compatible matrix")
@@ -263,8 +264,7 @@ def finalize_tiles(items: Sequence[FinalizeItem], *, tile_rows: int, keep_coeffi
         else:
             need(m["info"] == 0, "stored basis rows are singular", IntegrityError)
             ideal = min(1.0, float(m["traces"]) / source_energy)
-        low, high = fit_kernels.split_keys(m["extrema"], rank)
-        need(np.isfinite(low).all() and np.isfinite(high).all(), "coefficients must be finite")
+        need(finite[index], "coefficients must be finite")
         condition = _condition(float(m["eta"]), float(m["largest"]), rank, int(item.rows16.shape[1]), item.rows16)
         tiles.append((stored, residual, condition, ideal, source_energy, zero))
     codes = npk.quantize_many(coefficients, [m["extrema"] for m in measured], [item.spec for item in items])

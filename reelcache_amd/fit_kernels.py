@@ -189,6 +189,23 @@ def split_keys(keys_row, rank: int) -> tuple[np.ndarray, np.ndarray]:
     return decode_min_keys(row[:rank]), decode_max_keys(row[rank:2 * rank])
 
 
+def split_keys_many(keys_rows, ranks) -> tuple[list, list, list]:
+    """:func:`split_keys` of every row of a ``[n, width]`` key block at once (one vectorized decode
+    per rank): per row the fp32 (min, max) arrays and whether both are finite."""
+    rows = np.asarray(keys_rows)
+    lows, highs, finite = [None] * len(ranks), [None] * len(ranks), [False] * len(ranks)
+    by_rank: dict = {}
+    for index, rank in enumerate(ranks):
+        by_rank.setdefault(int(rank), []).append(index)
+    for rank, members in by_rank.items():
+        block = rows[members]
+        low, high = decode_min_keys(block[:, :rank]), decode_max_keys(block[:, rank:2 * rank])
+        ok = np.isfinite(low).all(1) & np.isfinite(high).all(1)
+        for position, index in enumerate(members):
+            lows[index], highs[index], finite[index] = low[position], high[position], bool(ok[position])
+    return lows, highs, finite
+
+
 def energies(sources, absmax_keys: torch.Tensor, *, bases=None, ranks=None, coefficients=None,
              residuals: bool = False):
     """float64 [n, 2]: sum (X/s)^2 and sum ((X - P Q)/s)^2 per source, s = max|X| from ``absmax_keys``

@@ -30,8 +30,8 @@ from typing import Any, Mapping, Sequence
 
 from ._checks import need
 from .errors import ConfigurationError, IntegrityError, UnsupportedError
-from .quantize import (MAX_DIMENSION, PIXEL_FORMATS, affine_from_extrema, expanded_affine, normalization_layout,
-                       video_layout)
+from .quantize import (MAX_DIMENSION, PIXEL_FORMATS, affine_from_extrema, covering_affine, expanded_affine,
+                       normalization_layout, video_layout)
 from .types import EncodedTensor, MatrixKey, TensorContext, json_copy
 
 __all__ = ["CANVAS_ALIGNMENT", "CANVAS_RANK_LADDER", "FACTOR_PACK_SCHEMA", "MIN_CANVAS", "PACK_SCHEMA",
@@ -167,21 +167,41 @@ def quantize_with_extrema(coefficients: torch.Tensor, keys_row, spec) -> tuple[t
 @torch.no_grad()
 def quantize_many(coefficients, keys, specs):
     """:func:`quantize_with_extrema` of many matrices (e.g. a chunk's) with one quantizer launch:
-    ``keys`` are the host extrema rows of ``fit_kernels.project(..., extrema=True)``.
+    ``keys`` are the host extrema rows of ``fit_kernels.project(..., extrema=True)`` (decoded
+    together; per-channel covering affines of equal rank computed together).
     Returns ``[(pixels, affine, layout)]``."""
-    affines, layouts, outputs, values = [], [], [], []
-    for p, row, spec in zip(coefficients, keys, specs):
+    ranks = []
+    for p in coefficients:
         _check(p)
-        rank = int(p.shape[1])
-        low, high = fit_kernels.split_keys(np.asarray(row), rank)
-        if not (np.isfinite(low).all() and np.isfinite(high).all()):
-            raise ConfigurationError("coefficients must be finite")
-        layout = normalization_layout(rank, spec.normalization, spec.protected_fraction)
-        affine = affine_from_extrema(low, high, layout)
+        ranks.append(int(p.shape[1]))
+    width = max((len(np.asarray(row)) for row in keys), default=0)
+    block = np.zeros((len(ranks), width), dtype=np.int64)
+    for index, row in enumerate(keys):
+        row = np.asarray(row)
+        block[index, :len(row)] = row
+    lows, highs, finite = fit_kernels.split_keys_many(block, ranks)
+    if not all(finite):
+        raise ConfigurationError("coefficients must be finite")
+    layouts = [normalization_layout(rank, spec.normalization, spec.protected_fraction)
+               for rank, spec in zip(ranks, specs)]
+    payloads: list = [None] * len(ranks)
+    per_channel: dict = {}
+    for index, layout in enumerate(layouts):
+        if layout["mode"] == "per_channel":
+            per_channel.setdefault(ranks[index], []).append(index)
+        else:
+            payloads[index] = affine_from_extrema(lows[index], highs[index], layout)
+    for members in per_channel.values():
+        # Elementwise covering affine of every per-channel matrix of one rank in one call.
+        covered = covering_affine(np.stack([lows[i] for i in members]), np.stack([highs[i] for i in members]))
+        for position, index in enumerate(members):
+            payloads[index] = np.ascontiguousarray(covered[:, position])
+    affines, outputs, values = [], [], []
+    for p, rank, layout, affine in zip(coefficients, ranks, layouts, payloads):
         scale, offset = expanded_affine(affine, layout, rank)
         affines.append(np.stack((np.asarray(scale, np.float64), np.asarray(offset, np.float64))))
-        layouts.append((affine.astype("<f4", copy=False), layout))
         values.append(p if p.stride(1) == 1 else p.contiguous())
+    layouts = [(affine.astype("<f4", copy=False), layout) for affine, layout in zip(payloads, layouts)]
     codes = fit_kernels.quantize_batched(values, affines)
     for pixels, (affine, layout) in zip(codes, layouts):
         outputs.append((pixels, affine, layout))
