@@ -179,8 +179,14 @@ def _rank_terms(coefficients, rows):
     else:  # tiles of different token counts: one product each
         products = torch.stack([c.double().T @ c.double() for c in coefficients])
     q64 = q.double()
-    factor, info = torch.linalg.cholesky_ex(torch.bmm(q64, q64.mT))
-    traces = torch.cholesky_solve(products, factor).diagonal(dim1=1, dim2=2).sum(-1)
+    gram = torch.bmm(q64, q64.mT)
+    if gram.shape[1] <= fit_kernels.CHOLESKY_MAX_K and gram.device.type == "cuda":
+        # G = R^T R, X = R^-1 (one launch for the group): trace(G^-1 C) = trace(X^T C X) = sum X * (C X).
+        inverse, info = fit_kernels.cholesky_inverse(gram)
+        traces = (inverse * torch.bmm(products, inverse)).sum((1, 2))
+    else:
+        factor, info = torch.linalg.cholesky_ex(gram)
+        traces = torch.cholesky_solve(products, factor).diagonal(dim1=1, dim2=2).sum(-1)
     q32 = q.float()
     gram32 = torch.bmm(q32, q32.mT)
     largest = gram32.diagonal(dim1=1, dim2=2).abs().amax(-1)

@@ -83,11 +83,11 @@ def _upload(table: np.ndarray, device: torch.device) -> torch.Tensor:
 
 
 def _fill_sources(table: np.ndarray, sources) -> None:
-    for row, x in zip(table, sources):
-        row["src_ptr"] = x.data_ptr()
-        row["src_dtype"] = _DTYPE_CODES[x.dtype]
-        row["rows"] = x.shape[0]
-        row["src_stride"] = x.stride(0)
+    """Source columns of a descriptor table, filled column by column (not row by row)."""
+    table["src_ptr"] = [x.data_ptr() for x in sources]
+    table["src_dtype"] = [_DTYPE_CODES[x.dtype] for x in sources]
+    table["rows"] = [x.shape[0] for x in sources]
+    table["src_stride"] = [x.stride(0) for x in sources]
 
 
 def decode_max_keys(keys) -> np.ndarray:
@@ -160,21 +160,25 @@ def project(sources, bases, ranks, *, extrema: bool = False):
     sizes = [int(x.shape[0]) * stride for x, stride in zip(aligned, strides)]
     storage = torch.empty(sum(sizes), dtype=torch.float32, device=device)  # every P of the batch, 16-byte rows
     first = 0
+    columns = {"basis_ptr": [], "basis_stride": [], "rank": [], "coef_ptr": []}
     for index, (x, basis, rank) in enumerate(zip(aligned, bases, ranks)):
         rank = int(rank)
         if not 1 <= rank <= basis.shape[0] or basis.shape[1] > c8 or basis.device != device:
             raise ConfigurationError("projection basis does not match its source")
         q = _aligned_basis(basis, rank, c8)
-        stride = strides[index]
-        p = storage[first:first + sizes[index]].view(int(x.shape[0]), stride)
+        p = storage[first:first + sizes[index]].view(int(x.shape[0]), strides[index])
         first += sizes[index]
         keep.append(q)
         outputs.append(p[:, :rank])
-        row = table[index]
-        row["basis_ptr"], row["basis_stride"], row["rank"] = q.data_ptr(), q.stride(0), rank
-        row["coef_ptr"], row["coef_stride"] = p.data_ptr(), stride
-        if extrema:
-            row["extrema_ptr"] = keys[index].data_ptr()
+        columns["basis_ptr"].append(q.data_ptr())
+        columns["basis_stride"].append(q.stride(0))
+        columns["rank"].append(rank)
+        columns["coef_ptr"].append(p.data_ptr())
+    for name, values in columns.items():
+        table[name] = values
+    table["coef_stride"] = strides
+    if extrema:
+        table["extrema_ptr"] = keys.data_ptr() + 4 * 2 * max_rank * np.arange(len(aligned))
     descriptors = _upload(table, device)
     max_rows = max(int(x.shape[0]) for x in aligned)
     _lib.call("rch_fit_project", descriptors.data_ptr(), len(aligned), c8, max_rows, max_rank,
@@ -234,6 +238,7 @@ def energies(sources, absmax_keys: torch.Tensor, *, bases=None, ranks=None, coef
             table[index]["resid_ptr"] = r.data_ptr()
             outputs.append(r[:, :sources[index].shape[1]])
     if with_basis:
+        columns = {"basis_ptr": [], "basis_stride": [], "rank": [], "coef_ptr": [], "coef_stride": []}
         for index, (x, basis, rank, p) in enumerate(zip(aligned, bases, ranks, coefficients)):
             rank = int(rank)
             if not 1 <= rank <= basis.shape[0] or p.shape != (x.shape[0], rank) or p.dtype != torch.float32:
@@ -245,9 +250,11 @@ def energies(sources, absmax_keys: torch.Tensor, *, bases=None, ranks=None, coef
                 copy[:, :rank].copy_(p)
                 p = copy
             keep += [q, p]
-            row = table[index]
-            row["basis_ptr"], row["basis_stride"], row["rank"] = q.data_ptr(), q.stride(0), rank
-            row["coef_ptr"], row["coef_stride"] = p.data_ptr(), p.stride(0)
+            for name, value in (("basis_ptr", q.data_ptr()), ("basis_stride", q.stride(0)), ("rank", rank),
+                                ("coef_ptr", p.data_ptr()), ("coef_stride", p.stride(0))):
+                columns[name].append(value)
+        for name, values in columns.items():
+            table[name] = values
     descriptors = _upload(table, device)
     _lib.call("rch_fit_residual", descriptors.data_ptr(), n, c8, max(int(x.shape[0]) for x in aligned),
               _DTYPE_CODES[aligned[0].dtype], _stream(device))
