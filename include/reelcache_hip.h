@@ -59,6 +59,8 @@ extern "C" {
 #define RCH_JF_SRC_VEC 1   /* coefficient rows: base and row stride 16-byte aligned, unit column stride */
 #define RCH_JF_DST_VEC 2   /* destination: unit dim stride, 16-byte aligned base and token/head strides, head_dim % 16 == 0 */
 #define RCH_JF_ROPE_VEC 4  /* RoPE tables: 16-byte aligned, row stride % 4 == 0, head_dim % 16 == 0 */
+#define RCH_JF_PIC_VEC4 8  /* pictures: every picture's base, the row and plane strides and grid_w are multiples
+                              of 4 bytes, so 4 tokens (x % 4 == 0) of a cell row are one aligned 32-bit word */
 
 /* Launch-group flags (rch_restore group_flags). */
 #define RCH_GF_FAST 1      /* every job: uint8 codes with RCH_JF_SRC_VEC or pictures, RCH_JF_DST_VEC,

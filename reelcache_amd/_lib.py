@@ -26,7 +26,7 @@ PRECISION_CODES = {"fp32": 0, "tf32": 1, "tf32x3": 2, "fp16": 3, "fp16x2": 4, "b
 DT_F32, DT_F16, DT_BF16, DT_U8, DT_F64 = 0, 1, 2, 3, 4
 SRC_FLOAT, SRC_U8, SRC_PICTURE, SRC_DENSE = 0, 1, 2, 3
 ROPE_NONE, ROPE_SEPARABLE, ROPE_DENSE = 0, 1, 2
-JF_SRC_VEC, JF_DST_VEC, JF_ROPE_VEC = 1, 2, 4
+JF_SRC_VEC, JF_DST_VEC, JF_ROPE_VEC, JF_PIC_VEC4 = 1, 2, 4, 8
 GF_FAST, GF_ROPE, GF_HEAD_PAIRS, GF_SPLIT_RANK, GF_STREAM, GF_DENSE_ROPE = 1, 2, 4, 8, 16, 32
 STREAM_SECTION_PAIRS = 2048
 

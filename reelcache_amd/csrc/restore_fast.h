@@ -258,30 +258,59 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
                                  static_cast<int64_t>(cell_col) * J->grid_w;
             }
             __syncthreads();
-            const int token = tid & (kTileTokens - 1), p = tid / kTileTokens;  // p is wave-uniform
-            constexpr int kParts = kThreadsT / kTileTokens;
-            const int64_t tt = t0 + token;
-            const bool live = tt < tokens;
-            const Coords c = coords(J, live ? static_cast<int>(tt) : 0);
             const RCH_GLOBAL uint8_t* base = gin<uint8_t>(J->src_ptr);
-            const int64_t lane = gin<int64_t>(J->pic_table_ptr)[c.f] + c.y * J->pic_row_stride + c.x;
-            uint8_t* row = codes + token * kPitch;
-            for (int b = p; 16 * b < kRanks; b += kParts) {
-                uint32_t got[16];
+            if (J->flags & RCH_JF_PIC_VEC4) {
+                // Aligned geometry: thread (quad, part) loads tokens 4 quad .. + 3 (one cell-row word:
+                // x % 4 == 0 and grid_w % 4 == 0 keep them in one row) of ranks 4 g .. 4 g + 3 for the
+                // groups g of its part, and transposes the 4 x 4 bytes into 4 tokens' rank words.
+                constexpr int kQuads = kTileTokens / 4, kParts4 = kThreadsT / kQuads;
+                const int quad = tid % kQuads, part = tid / kQuads;
+                const int64_t tt = t0 + 4 * quad;
+                const bool live = tt < tokens;  // tokens % 4 == 0: a quad is whole or past the end
+                const Coords c = coords(J, live ? static_cast<int>(tt) : 0);
+                const int64_t lane = gin<int64_t>(J->pic_table_ptr)[c.f] + c.y * J->pic_row_stride + c.x;
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int k = 16 * b + i;
-                    const bool take = live & (k < rank);
-                    got[i] = base[take ? lane + cell_offset[k] : 0];  // byte 0 of the first picture is readable
-                    got[i] = take ? got[i] : 0u;
+                for (int g = part; 4 * g < kRanks; g += kParts4) {
+                    uint32_t d[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int k = 4 * g + r;
+                        const bool take = live & (k < rank);
+                        d[r] = *reinterpret_cast<const RCH_GLOBAL uint32_t*>(base + (take ? lane + cell_offset[k] : 0));
+                        d[r] = take ? d[r] : 0u;  // word 0 of the first picture is readable
+                    }
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const uint32_t word = ((d[0] >> (8 * t)) & 0xffu) | (((d[1] >> (8 * t)) & 0xffu) << 8) |
+                                              (((d[2] >> (8 * t)) & 0xffu) << 16) | (((d[3] >> (8 * t)) & 0xffu) << 24);
+                        *reinterpret_cast<uint32_t*>(codes + (4 * quad + t) * kPitch + 4 * g) = word;
+                    }
                 }
-                u4 word;
+            } else {
+                const int token = tid & (kTileTokens - 1), p = tid / kTileTokens;  // p is wave-uniform
+                constexpr int kParts = kThreadsT / kTileTokens;
+                const int64_t tt = t0 + token;
+                const bool live = tt < tokens;
+                const Coords c = coords(J, live ? static_cast<int>(tt) : 0);
+                const int64_t lane = gin<int64_t>(J->pic_table_ptr)[c.f] + c.y * J->pic_row_stride + c.x;
+                uint8_t* row = codes + token * kPitch;
+                for (int b = p; 16 * b < kRanks; b += kParts) {
+                    uint32_t got[16];
 #pragma unroll
-                for (int w = 0; w < 4; ++w)
-                    word[w] = got[4 * w] | (got[4 * w + 1] << 8) | (got[4 * w + 2] << 16) | (got[4 * w + 3] << 24);
-                u2* out = reinterpret_cast<u2*>(row + 16 * b);
-                out[0] = u2{word[0], word[1]};
-                out[1] = u2{word[2], word[3]};
+                    for (int i = 0; i < 16; ++i) {
+                        const int k = 16 * b + i;
+                        const bool take = live & (k < rank);
+                        got[i] = base[take ? lane + cell_offset[k] : 0];  // byte 0 of the first picture is readable
+                        got[i] = take ? got[i] : 0u;
+                    }
+                    u4 word;
+#pragma unroll
+                    for (int w = 0; w < 4; ++w)
+                        word[w] = got[4 * w] | (got[4 * w + 1] << 8) | (got[4 * w + 2] << 16) | (got[4 * w + 3] << 24);
+                    u2* out = reinterpret_cast<u2*>(row + 16 * b);
+                    out[0] = u2{word[0], word[1]};
+                    out[1] = u2{word[2], word[3]};
+                }
             }
         } else {  // pictures of several segments: one thread per (token, half of the rank columns)
             const int token = tid >> 1, half = tid & 1;

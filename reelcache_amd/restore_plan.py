@@ -368,7 +368,7 @@ class _JobDesc:
 
     __slots__ = ("affine", "basis", "basis_key", "channels", "dst", "dst_shift", "dst_vec_rule", "dtype",
                  "exponent", "grid", "head_dim", "host_bound", "key", "key_id", "kind", "out_dtype", "pictures",
-                 "rank", "rope_kind", "row", "section_pairs", "src", "src_vec_rule", "table", "tokens")
+                 "rank", "rope_kind", "row", "section_pairs", "src", "src_vec_rule", "table", "tokens", "pic_vec_rule")
 
     def __init__(self, job):
         view, source = job.destination, job.source
@@ -385,6 +385,7 @@ class _JobDesc:
         self.dtype = _DTYPE_CODES[dtype]
         self.src = self.pictures = self.basis = self.basis_key = self.affine = self.host_bound = None
         self.src_vec_rule, self.rank, self.exponent = False, 0, 0
+        self.pic_vec_rule = False
         if isinstance(source, DenseSource):
             self.src = source.values
             row[_C_SRC_DTYPE] = self.dtype
@@ -447,6 +448,8 @@ class _JobDesc:
             row[_C_PIC_SLOTS], row[_C_PIC_PLANES] = layout["channels_per_segment"], layout["planes"]
             row[_C_PIC_COLS] = layout["grid"][0]
             row[_C_PIC_PLANE_STRIDE], row[_C_PIC_ROW_STRIDE] = source.plane_stride, source.row_stride
+            # Word gathers (4 tokens of a cell row per 32-bit load) when the geometry keeps them aligned.
+            self.pic_vec_rule = source.plane_stride % 4 == 0 and source.row_stride % 4 == 0 and job.grid[2] % 4 == 0
             self._affine(source.scale, source.offset)
             return
         values = self.src = source.values
@@ -893,6 +896,7 @@ def run_call(descs, device, stream, precision, config, keepalive, stage_events=N
     src = [desc.source_address() for desc in descs]
     dynamic = [(_lib.JF_DST_VEC if desc.dst_vec_rule and not d & 15 else 0)
                | (_lib.JF_SRC_VEC if desc.src_vec_rule and not s & 15 else 0)
+               | (_lib.JF_PIC_VEC4 if desc.pic_vec_rule and all(not p.data_ptr() & 3 for p in desc.pictures) else 0)
                for desc, d, s in zip(descs, dst, src)]
     bases, groups, first_of = [0] * len(descs), [None] * len(descs), {}
     for index, desc in enumerate(descs):

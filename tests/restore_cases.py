@@ -53,7 +53,8 @@ def destination(layout, tokens, heads, head_dim, dtype, device, *, offset=0, ext
 
 def make_case(rng, *, grid, heads, head_dim, rank, basis_rows=None, source="uint8", rope="separable",
               layout="BTHD", out_dtype="bfloat16", device="cpu", basis_dtype=torch.float16, token_offset=0,
-              view=None, basis=None, table=None, rope_rows=None, coefficient_dtype=torch.float32, code_pitch=None):
+              view=None, basis=None, table=None, rope_rows=None, coefficient_dtype=torch.float32, code_pitch=None,
+              picture_origin=(2, 3), picture_pad=(3, 5)):
     """One job with random inputs; ``view`` (a NativeView) overrides the destination.
 
     ``code_pitch``: uint8 codes live in the first ``rank`` columns of ``[N, code_pitch]`` rows
@@ -80,9 +81,9 @@ def make_case(rng, *, grid, heads, head_dim, rank, basis_rows=None, source="uint
             src = rk.CoefficientSource(values, scale, offset)
         else:
             layout_v1 = oq.video_layout(grid[0], grid[1], grid[2], rank, "yuv444p")
-            canvas, indices = orc.pack_pictures(codes, layout_v1, origin=(2, 3))
-            src = rk.PictureSource.from_canvases(torch.from_numpy(canvas).to(device), layout_v1, indices, (2, 3),
-                                                 scale, offset)
+            canvas, indices = orc.pack_pictures(codes, layout_v1, origin=picture_origin, pad=picture_pad)
+            src = rk.PictureSource.from_canvases(torch.from_numpy(canvas).to(device), layout_v1, indices,
+                                                 tuple(picture_origin), scale, offset)
     elif source == "float":
         values = torch.from_numpy(rng.standard_normal((tokens, rank)).astype(np.float32) * 3).to(coefficient_dtype)
         coefficients = values.float().numpy()

@@ -19,6 +19,8 @@ from oracle import restore as orc
 from reelcache_amd import restore_kernels as rk
 from reelcache_amd.errors import ConfigurationError
 from reelcache_amd.factorization import basis_condition_bound, fast_condition_bound
+from reelcache_amd.restore_plan import job_desc
+from restore_cases import make_case
 
 
 # ---------------------------------------------------------------------------
@@ -169,3 +171,17 @@ def test_product_coefficient_bounds_match_the_oracle():
     offsets = [rng.standard_normal(r).astype(np.float32) * 5 for r in ranks]
     for s, o in zip(scales, offsets):
         assert rk._coefficient_bound(s, o) == orc.coefficient_bound(s, o)
+
+
+@pytest.mark.parametrize("origin,pad,grid,aligned", [((0, 0), (3, 4), (3, 30, 52), True),
+                                                     ((2, 4), (3, 4), (3, 30, 52), True),
+                                                     ((2, 3), (3, 5), (3, 30, 52), False),   # odd origin and stride
+                                                     ((0, 0), (3, 4), (2, 12, 14), False)])  # cell width 14
+def test_picture_word_gather_rule(origin, pad, grid, aligned):
+    """A picture matrix takes the 32-bit word gather only when every cell-row start is
+    4-byte aligned: plane and row strides and the cell width multiples of 4 (the job rule),
+    and every picture view's address a multiple of 4 (checked per call)."""
+    case = make_case(np.random.default_rng(3), grid=grid, heads=4, head_dim=32, rank=96, source="pictures",
+                     rope="none", out_dtype="bfloat16", device="cpu", picture_origin=origin, picture_pad=pad)
+    desc = job_desc(case.job)
+    assert (desc.pic_vec_rule and all(p.data_ptr() % 4 == 0 for p in desc.pictures)) == aligned

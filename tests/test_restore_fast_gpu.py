@@ -122,6 +122,30 @@ def test_unaligned_jobs_use_the_general_kernel(device):
     _check_bound(case, "fp16x2")
 
 
+@pytest.mark.parametrize("grid,rank,heads,rope", [((2, 12, 16), 96, 4, "none"),        # one segment, 4-aligned
+                                                  ((3, 30, 52), 192, 2, "separable")])  # CausVid cells, rank 192
+def test_fast_picture_word_gather(device, grid, rank, heads, rope):
+    """Pictures whose geometry is 4-byte aligned (origin x and grid_w multiples of 4, aligned
+    strides) take the word gather (4 tokens x 4 ranks per set of 32-bit loads, transposed in
+    registers); the same codes at an unaligned origin take the byte gather.  Both equal the
+    general kernel bit for bit and stay within the oracle's bound."""
+    from reelcache_amd.restore_plan import job_desc
+
+    cases = []
+    for origin, pad in (((0, 0), (3, 4)), ((0, 0), (3, 4)), ((2, 3), (3, 5))):
+        rng = np.random.default_rng(59)
+        cases.append(make_case(rng, grid=grid, heads=heads, head_dim=128 if rank == 192 else 32, rank=rank,
+                               source="pictures", rope=rope, out_dtype="bfloat16", device=device, picture_origin=origin,
+                               picture_pad=pad))
+    assert job_desc(cases[0].job).pic_vec_rule and all(p.data_ptr() % 4 == 0 for p in job_desc(cases[0].job).pictures)
+    assert _run(cases[0], "fp16x2", "pairs") == ["pairs"]
+    assert _run(cases[1], "fp16x2", "general") == ["general"]
+    assert _run(cases[2], "fp16x2", "pairs") == ["pairs"]
+    assert np.array_equal(written(cases[0]), written(cases[1]))
+    assert np.array_equal(written(cases[2]), written(cases[1]))
+    _check_bound(cases[0], "fp16x2")
+
+
 # (heads, head_dim, rank, rope, grid): ranks beyond one wave's registers (rank halves)
 SPLIT_SHAPES = [
     (4, 128, 200, "separable", (2, 9, 13)),   # fp16x2: 13 steps -> halves of 8
