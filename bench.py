@@ -679,8 +679,8 @@ def main():
                              "dispatches for rocprofv3 FETCH_SIZE / WRITE_SIZE passes)")
     args = parser.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only; the restore shards by layer or head with no "
-                                   "exchange (see DESIGN.md), run with --gpus 1"}))
+        print(json.dumps({"error": "this build measures one GPU only (the restore would shard by layer or head "
+                                   "with no exchange between GPUs); run with --gpus 1"}))
         sys.exit(2)
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)

@@ -8,8 +8,8 @@
  * synchronizes the stream or changes process-wide state.
  *
  * The Python host (reelcache_amd/restore_kernels.py, reelcache_amd/gpu_fitting.py)
- * binds these symbols with ctypes; a reference-side binding is shown in
- * INTEGRATION.md.  Each declaration names the reference interface it replaces.
+ * binds these symbols with ctypes (reelcache_amd/_lib.py lists every signature).  Each
+ * declaration names the reference interface it replaces.
  */
 #ifndef REELCACHE_HIP_H
 #define REELCACHE_HIP_H
