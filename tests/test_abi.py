@@ -46,3 +46,24 @@ def test_header_struct_fields_match_the_binding():
                 names.extend(part.strip().split()[-1] for part in declaration.split(","))
         assert len(names) == len(fields), struct
         assert [n for n in names if not n.startswith("reserved")] == [f for f in fields if not f.startswith("reserved")]
+
+
+def test_header_constants_match_the_binding():
+    """Status, precision, dtype, source, RoPE, job-flag and group-flag codes of the header ==
+    the values the ctypes binding writes into descriptors and passes to the entry points."""
+    defines = {name: int(value) for name, value in
+               re.findall(r"#define (RCH_[A-Z0-9_]+) (\d+)\b", HEADER.read_text())}
+    expected = {"RCH_E_CONFIG": _lib.E_CONFIG, "RCH_E_UNSUPPORTED": _lib.E_UNSUPPORTED, "RCH_E_LAUNCH": _lib.E_LAUNCH,
+                "RCH_DT_F32": _lib.DT_F32, "RCH_DT_F16": _lib.DT_F16, "RCH_DT_BF16": _lib.DT_BF16,
+                "RCH_DT_U8": _lib.DT_U8, "RCH_DT_F64": _lib.DT_F64,
+                "RCH_SRC_FLOAT": _lib.SRC_FLOAT, "RCH_SRC_U8": _lib.SRC_U8, "RCH_SRC_PICTURE": _lib.SRC_PICTURE,
+                "RCH_SRC_DENSE": _lib.SRC_DENSE,
+                "RCH_ROPE_NONE": _lib.ROPE_NONE, "RCH_ROPE_SEPARABLE": _lib.ROPE_SEPARABLE,
+                "RCH_ROPE_DENSE": _lib.ROPE_DENSE,
+                "RCH_JF_SRC_VEC": _lib.JF_SRC_VEC, "RCH_JF_DST_VEC": _lib.JF_DST_VEC,
+                "RCH_JF_ROPE_VEC": _lib.JF_ROPE_VEC, "RCH_JF_PIC_VEC4": _lib.JF_PIC_VEC4,
+                "RCH_GF_FAST": _lib.GF_FAST, "RCH_GF_ROPE": _lib.GF_ROPE, "RCH_GF_HEAD_PAIRS": _lib.GF_HEAD_PAIRS,
+                "RCH_GF_SPLIT_RANK": _lib.GF_SPLIT_RANK, "RCH_GF_STREAM": _lib.GF_STREAM,
+                "RCH_GF_DENSE_ROPE": _lib.GF_DENSE_ROPE}
+    expected.update({"RCH_PREC_" + name.upper(): code for name, code in _lib.PRECISION_CODES.items()})
+    assert {name: defines.get(name) for name in expected} == expected
