@@ -138,7 +138,8 @@ typedef struct rch_pack {
     int64_t channels;
     int64_t dst_ptr;         /* RCH_PACK_FRAGMENTS: ksteps * nblocks * 64 * frag bytes;
                                 RCH_PACK_STREAM: nblocks slabs of RCH_STREAM_SLAB_BYTES(ksteps) */
-    int64_t ksteps;          /* fragments: ceil(rank / 16); stream slabs: the kernel's rank steps (>= ceil(rank / 16)) */
+    int64_t ksteps;          /* fragments: ceil(rank / 16); stream slabs: the stream kernel's rank steps,
+                                exactly 4, 8, 12 or 16 and >= ceil(rank / 16) (other depths: no slab written) */
     int64_t nblocks;         /* fragments: 2 * ceil(channels / 64); stream slabs: channels / 32 */
     int64_t kind;            /* RCH_PACK_* */
     int64_t exp_ptr;         /* fragments: device int32 [nblocks], per 32-channel-block prescale exponents written here */
@@ -265,7 +266,10 @@ int rch_restore_sliced(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles
  *               fragment region, size = ksteps * nblocks * 64 * rch_fragment_bytes(precision) for
  *               RCH_PACK_FRAGMENTS and nblocks * RCH_STREAM_SLAB_BYTES(ksteps) for RCH_PACK_STREAM;
  *               fragment packs' block exponents go to word E_i = sum of nblocks over the earlier
- *               fragment packs.
+ *               fragment packs.  Every pack's kind matches the group's kernel: stream slabs
+ *               (RCH_GF_STREAM groups only) have ksteps equal to the stream variant that covers
+ *               max_ksteps (4, 8, 12 or 16); fragment packs have ksteps = ceil(rank / 16).
+ *               Anything else returns RCH_E_CONFIG before any launch.
  *   jobs_dev    as for rch_restore, except that a job of pack i carries pack_ptr = F_i (relative to
  *               the fragment region) and basis_exp_index = E_i, and bound_index = -1 (no device
  *               coefficient bounds: float sources in the fp16 modes need a host bound).

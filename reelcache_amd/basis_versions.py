@@ -79,7 +79,10 @@ def rows_from_bytes(data: bytes, rows: int, channels: int) -> torch.Tensor:
 
 
 def _canonical(value) -> bytes:
-    return json.dumps(value, sort_keys=True, separators=(",", ":"), allow_nan=False).encode("utf-8")
+    """Manifest bytes: sorted keys, no whitespace, no NaN, and non-ASCII text as raw UTF-8 (not
+    ``\\u`` escapes), as the reference store writes them (reelcache/serialization.py:31-34)."""
+    return json.dumps(value, sort_keys=True, separators=(",", ":"), ensure_ascii=False,
+                      allow_nan=False).encode("utf-8")
 
 
 def object_ref(value: Any, name: str, *, kinds: tuple = ("manifest",)) -> str:

@@ -175,13 +175,20 @@ __device__ __forceinline__ void stream_slab_group(const rch_pack& P) {
     if (lane == 0) gout<int32_t>(slab + KS * 2048 + 128)[0] = e;
 }
 
+// The slab depths the stream kernel is compiled for (restore_stream.hip); slabs of any other depth
+// are neither written nor read.
+__host__ __device__ constexpr bool stream_pack_steps(int64_t steps) {
+    return steps == 4 || steps == 8 || steps == 12 || steps == 16;
+}
+
 template <int DT>
 __device__ __forceinline__ void stream_slab_steps(const rch_pack& P, int steps) {
     switch (steps) {
         case 4: stream_slab_group<4, DT>(P); break;
         case 8: stream_slab_group<8, DT>(P); break;
         case 12: stream_slab_group<12, DT>(P); break;
-        default: stream_slab_group<16, DT>(P); break;
+        case 16: stream_slab_group<16, DT>(P); break;
+        default: break;  // refused: no slab is written past what the caller sized
     }
 }
 
@@ -189,7 +196,8 @@ template <int PREC>
 __device__ __forceinline__ void basis_pack_body(const rch_pack P) {
     if (P.kind == RCH_PACK_STREAM) {
         // Four blocks per workgroup, one per wave; only the y == 0 row of the grid.
-        if (blockIdx.y != 0 || 4 * static_cast<int64_t>(blockIdx.x) >= P.nblocks) return;
+        if (blockIdx.y != 0 || 4 * static_cast<int64_t>(blockIdx.x) >= P.nblocks || !stream_pack_steps(P.ksteps))
+            return;
         const int steps = static_cast<int>(P.ksteps);
         switch (static_cast<int>(P.src_dtype)) {
             case RCH_DT_F32: stream_slab_steps<RCH_DT_F32>(P, steps); break;
@@ -639,6 +647,10 @@ int rch_restore_noalloc(const rch_pack* packs_host, int n_packs, const rch_job* 
     // F_i = sum_{j<i} round_up(ksteps_j * nblocks_j * 64 * fragment bytes, 256) of the fragment region.
     const int64_t fragment = rch_fragment_bytes(precision);
     int64_t words = 0, bytes = 0, max_nblocks = 0, max_pack_steps = 0;
+    // The kernel first: a stream variant reads slabs of exactly its own ks rank steps.
+    Launch launch;
+    status = pick_launch(precision, source_kind, max_ksteps, head_dim, out_dtype, group_flags, &launch);
+    if (status) return status;
     PackArgs args;
     void* base = nullptr;
     status = current_scratch(&base);
@@ -648,11 +660,13 @@ int rch_restore_noalloc(const rch_pack* packs_host, int n_packs, const rch_job* 
     for (int i = 0; i < n_packs; ++i) {
         const rch_pack& P = packs_host[i];
         const bool slabs = P.kind == RCH_PACK_STREAM;
-        if (P.rank <= 0 || P.channels <= 0 || (P.kind != RCH_PACK_FRAGMENTS && !slabs) ||
-            (slabs ? (P.ksteps < (P.rank + 15) / 16 || P.ksteps > 16 || P.nblocks != P.channels / 32 || P.channels % 128)
+        if (P.rank <= 0 || P.channels <= 0 || (P.kind != RCH_PACK_FRAGMENTS && !slabs) || slabs != launch.stream ||
+            (slabs ? (!stream_pack_steps(P.ksteps) || P.ksteps != launch.ks || P.ksteps < (P.rank + 15) / 16 ||
+                      P.nblocks != P.channels / 32 || P.channels % 128)
                    : (P.ksteps != (P.rank + 15) / 16 || P.nblocks != 2 * ((P.channels + 63) / 64))))
             return fail(RCH_E_CONFIG, "rch_restore_noalloc: pack %d: kind / ksteps / nblocks do not match its rank / "
-                        "channels", i);
+                        "channels or the launch group's kernel (stream slabs: ksteps 4, 8, 12 or 16, the variant's)",
+                        i);
         args.pack[i] = P;
         args.pack[i].exp_ptr = word_base + 4 * words;
         args.pack[i].dst_ptr = fragment_base + bytes;
@@ -668,9 +682,6 @@ int rch_restore_noalloc(const rch_pack* packs_host, int n_packs, const rch_job* 
                     "static scratch holds %d and %d",
                     static_cast<long long>(bytes), static_cast<long long>(words),
                     RCH_NOALLOC_SCRATCH_BYTES - RCH_NOALLOC_WORD_BYTES, RCH_NOALLOC_WORD_BYTES / 4);
-    Launch launch;
-    status = pick_launch(precision, source_kind, max_ksteps, head_dim, out_dtype, group_flags, &launch);
-    if (status) return status;
     hipStream_t s = as_stream(stream);
     const dim3 pack_grid(static_cast<unsigned>((max_nblocks + 1) / 2), static_cast<unsigned>((max_pack_steps + 1) / 2),
                          static_cast<unsigned>(n_packs));

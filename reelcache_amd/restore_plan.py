@@ -755,13 +755,19 @@ class _Layout:
             total += pack["bytes"]
             words += pack["nblocks"] if pack["kind"] == _lib.PACK_FRAGMENTS else 0
         self.exp_words = words
+        # Static scratch: each launch group packs its own bases at the start of the library's array,
+        # in the order of ``plan["packs"]``, so a pack's position is a property of the (group, pack)
+        # pair: one basis can sit at different positions in two groups (ranks in two rank classes).
+        static_at = {}
         if self.static:
             total = 0
             for plan in plans:
                 fragment_at, word_at = 0, 0
-                for index in plan.get("packs", ()):
-                    pack = packs[index]
-                    pack["static_offset"], pack["static_word"] = fragment_at, word_at
+                for pack_index in plan.get("packs", ()):
+                    pack = packs[pack_index]
+                    for member in plan["members"]:
+                        if pack_of.get(member) == pack_index:
+                            static_at[member] = (fragment_at, word_at)
                     fragment_at += pack["bytes"]
                     word_at += pack["nblocks"] if pack["kind"] == _lib.PACK_FRAGMENTS else 0
         self.pack_total = total
@@ -771,7 +777,7 @@ class _Layout:
             pack = packs[pack_index]
             rows[index, _C_PACK_NBLOCKS] = pack["nblocks"]
             if self.static:
-                rows[index, _C_PACK_PTR], rows[index, _C_EXP_INDEX] = pack["static_offset"], pack["static_word"]
+                rows[index, _C_PACK_PTR], rows[index, _C_EXP_INDEX] = static_at[index]
             else:
                 rows[index, _C_EXP_INDEX] = pack["word"]
                 relative[index, _C_PACK_PTR] = 1  # the buffer offset is known once the arena is complete

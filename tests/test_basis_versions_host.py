@@ -128,3 +128,22 @@ def test_detach_and_attach_single_matrix_basis():
         bv.attach_basis(header, payloads, bytes(len(raw)), rank_view=4, channels=48)
     with pytest.raises(IntegrityError):
         bv.attach_basis(header, payloads, raw, rank_view=3, channels=48)
+
+
+def test_manifests_keep_non_ascii_text_as_utf8():
+    """The manifest bytes of a version whose model fingerprint is not ASCII hold the fingerprint's
+    UTF-8 bytes, not JSON \\u escapes, so its ``manifest:<sha256>`` address is the reference store's
+    (reelcache/serialization.py:31-34 writes ensure_ascii=False)."""
+    model = ModelIdentity("versions-test", "modèle-vidéo-ü", 2, {"K": 16, "V": 16}, "THD", "bfloat16")
+    store = bv.MemoryObjectStore()
+    versions = bv.BasisVersionStore(store, model)
+    ref, version = versions.put_root(MatrixKey(0, "K"), _rows(np.random.default_rng(9), 3, 16))
+    assert version.model_fingerprint == model.fingerprint
+    data = store.get(ref)
+    assert model.fingerprint.encode("utf-8") in data and b"\\u00e8" not in data
+    # The address is the SHA-256 of exactly those bytes, and re-encoding the parsed record the
+    # reference's way gives the same bytes.
+    assert ref == "manifest:" + hashlib.sha256(data).hexdigest()
+    parsed = json.loads(data.decode("utf-8"))
+    assert json.dumps(parsed, sort_keys=True, separators=(",", ":"), ensure_ascii=False,
+                      allow_nan=False).encode("utf-8") == data

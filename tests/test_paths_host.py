@@ -20,7 +20,7 @@ from reelcache_amd import restore_kernels as rk
 from reelcache_amd.errors import ConfigurationError
 from reelcache_amd.factorization import basis_condition_bound, fast_condition_bound
 from reelcache_amd.restore_plan import job_desc
-from restore_cases import make_case
+from restore_cases import make_case, orthonormal_basis
 
 
 # ---------------------------------------------------------------------------
@@ -185,3 +185,54 @@ def test_picture_word_gather_rule(origin, pad, grid, aligned):
                      rope="none", out_dtype="bfloat16", device="cpu", picture_origin=origin, picture_pad=pad)
     desc = job_desc(case.job)
     assert (desc.pic_vec_rule and all(p.data_ptr() % 4 == 0 for p in desc.pictures)) == aligned
+
+
+def _noalloc_placement(group_packs, fragment_bytes):
+    """Where rch_restore_noalloc puts a launch group's packs (csrc/restore.hip): pack i's fragments
+    at byte sum_{j<i} round_up(ksteps_j * nblocks_j * 64 * fragment, 256) of the fragment region, its
+    block exponents at word sum_{j<i} nblocks_j (fragment packs)."""
+    places, at, word = [], 0, 0
+    for pack in group_packs:
+        places.append((at, word))
+        at += (int(pack["ksteps"]) * int(pack["nblocks"]) * 64 * fragment_bytes + 255) // 256 * 256
+        word += int(pack["nblocks"])
+    return places
+
+
+def test_static_scratch_rows_point_at_their_own_group_packs(monkeypatch):
+    """One basis used by two launch groups at different positions (two rank classes): every job's
+    pack pointer and exponent word must name where its own group's no-allocation call packs it."""
+    from reelcache_amd import restore_plan as rp
+
+    monkeypatch.setattr(rp, "_compute_units", lambda device: 256)
+    monkeypatch.setattr(rp, "_occupancy", lambda *args: 2)
+    rng = np.random.default_rng(5)
+    heads = 2
+    basis_x = orthonormal_basis(128, heads * 128, rng)
+    basis_y = orthonormal_basis(192, heads * 128, rng)
+    # Group 1 (8 rank steps): A on X, B on Y -> packs [X, Y].  Group 2 (4 steps): C on Y -> [Y].
+    cases = [make_case(rng, grid=(1, 4, 8), heads=heads, head_dim=128, rank=rank, rope="none", basis=basis)
+             for rank, basis in ((128, basis_x), (120, basis_y), (40, basis_y))]
+    descs = [job_desc(case.job) for case in cases]
+    dynamic = [rp._lib.JF_DST_VEC | rp._lib.JF_SRC_VEC] * len(descs)
+    groups = [0, 1, 1]
+    config = {**rp.DEFAULT_MERGED, "static_scratch": True}
+    layout = rp._Layout(descs, dynamic, groups, "fp16x2", config, "cpu")
+    assert len(layout.plans) == 2
+    pack_group = {}  # job -> index of its basis pack in the layout's pack table
+    for position, member in enumerate(layout.pack_sources):
+        for job, group in enumerate(groups):
+            if group == groups[member]:
+                pack_group[job] = position
+    checked = 0
+    for plan in layout.plans:
+        group_packs = layout.pack_rows[plan["packs"]]
+        fields = {name: group_packs[:, rp._PACK_COLUMN[name]] for name in ("ksteps", "nblocks")}
+        places = _noalloc_placement([{k: v[i] for k, v in fields.items()} for i in range(len(group_packs))], 16)
+        for job in plan["members"]:
+            where = plan["packs"].index(pack_group[job])
+            assert (layout.rows[job, rp._C_PACK_PTR], layout.rows[job, rp._C_EXP_INDEX]) == places[where]
+            checked += 1
+    assert checked == 3
+    # Job C (group 2) reads basis Y at the start of the array; job B (group 1) after X's fragments.
+    assert layout.rows[2, rp._C_PACK_PTR] == 0 and layout.rows[1, rp._C_PACK_PTR] > 0

@@ -65,6 +65,24 @@ def test_noalloc_matches_the_allocating_entry_points(device):
         assert float((np.abs(b - values) - bound).max()) <= 0
 
 
+def test_noalloc_with_one_basis_in_two_launch_groups(device):
+    """One basis shared by jobs of two rank classes (two launch groups) at different pack positions
+    in each group: the no-allocation call must read each group's own copy."""
+    rng = np.random.default_rng(73)
+    heads = 4
+    first = torch.from_numpy(np.linalg.qr(rng.standard_normal((heads * 128, 128)))[0].T.copy()).to(torch.bfloat16)
+    second = torch.from_numpy(np.linalg.qr(rng.standard_normal((heads * 128, 192)))[0].T.copy()).to(torch.bfloat16)
+    first, second = first.to(device), second.to(device)
+    cases = [make_case(rng, grid=(1, 6, 9), heads=heads, head_dim=128, rank=rank, source="uint8", rope="none",
+                       device=device, basis=basis)
+             for rank, basis in ((128, first), (120, second), (40, second), (56, first))]
+    one, two = _pair(cases)
+    for case, a, b in zip(cases, one, two):
+        np.testing.assert_array_equal(a, b)
+        values, bound = expected(case, "fp16x2")
+        assert float((np.abs(b - values) - bound).max()) <= 0
+
+
 def _pack(rank, channels):
     pack = np.zeros(1, dtype=_lib.PACK_DTYPE)
     pack["src_dtype"], pack["rank"], pack["channels"], pack["row_stride"] = _lib.DT_F16, rank, channels, channels
@@ -84,4 +102,16 @@ def test_noalloc_refuses_sizes_beyond_the_array(device):
     with pytest.raises(ConfigurationError, match="at most 8"):
         _lib.call("rch_restore_noalloc", many.ctypes.data, 9, address, 1, address, 1, address, 1, 128, 128,
                   _lib.SRC_U8, _lib.DT_BF16, 4, 1, 0, stream)
+    # Stream slabs must have the depth of the stream variant that runs (4, 8, 12 or 16 rank steps):
+    # these are refused before anything is launched.
+    fp16x2, flags = _lib.PRECISION_CODES["fp16x2"], _lib.GF_FAST | _lib.GF_STREAM
+    for ksteps, max_ksteps in ((6, 6), (8, 10), (16, 4)):
+        slab = _pack(16 * max_ksteps, 256)
+        slab["kind"], slab["ksteps"], slab["nblocks"] = _lib.PACK_STREAM, ksteps, 8
+        with pytest.raises(ConfigurationError, match="stream slabs"):
+            _lib.call("rch_restore_noalloc", slab.ctypes.data, 1, address, 1, address, 1, address, 1, 256, 128,
+                      _lib.SRC_U8, _lib.DT_BF16, fp16x2, max_ksteps, flags, stream)
+    with pytest.raises(ConfigurationError, match="stream slabs"):  # fragments in a stream group
+        _lib.call("rch_restore_noalloc", _pack(64, 256).ctypes.data, 1, address, 1, address, 1, address, 1, 256,
+                  128, _lib.SRC_U8, _lib.DT_BF16, fp16x2, 4, flags, stream)
     torch.cuda.synchronize(device)
