@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-#define RCH_ABI_VERSION 8
+#define RCH_ABI_VERSION 9
 
 /* Status codes (mapped to reelcache errors by the host). */
 #define RCH_OK 0
@@ -292,6 +292,33 @@ int rch_restore_noalloc(const rch_pack* packs_host, int n_packs, const rch_job* 
  */
 int rch_rope_store(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev, int n_tiles,
                    int channels, int head_dim, int out_dtype, void* stream);
+
+/*
+ * Staged comparison path (backend="staged"), one GEMM group at a time: the jobs of tiles_dev share
+ * one basis and rank view, and their coefficient rows stack into one dense [rows, rank] work
+ * matrix, job j's token t at row rows_dev[j] + t (int64 [n_jobs]; entries of other jobs unused).
+ *
+ * rch_staged_unpack writes that matrix: coefficients dequantized as float(q) * scale + offset with
+ * two roundings (uint8 rows, pictures) or read as is (float sources), in the fp16 precision times
+ * the job's power-of-two prescale 2^e (coef_exp, or the device bound's exponent when bound_index
+ * >= 0: rch_coefficient_bound runs first), then rounded once to work_dtype (RCH_DT_F32 / F16 /
+ * BF16).  tiles_dev: int32 [n_tiles][2] (job, first token) of 128-token tiles; work_stride in
+ * elements, >= max_rank.  Replaces _unpack_kernel (reelcache/restore_kernels.py:1518-1554) as
+ * _staged_group launches it (:2192-2230).
+ *
+ * The caller multiplies work @ Q[:rank] with the GPU BLAS library into an fp32 [rows, channels]
+ * product (the reference's _staged_gemm, :2167-2189).
+ *
+ * rch_staged_store reads product row rows_dev[j] + t, multiplies by 2^-e (fp16), applies the job's
+ * RoPE, casts and stores into the native slot.  Replaces _rope_store_kernel with PRESCALE as
+ * _staged_group launches it (:1557-1585, :2244-2247).  precision: RCH_PREC_FP32, _FP16 or _BF16.
+ */
+int rch_staged_unpack(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev, int n_tiles,
+                      const int64_t* rows_dev, void* work, int64_t work_stride, int max_rank, int source_kind,
+                      int work_dtype, int precision, const int32_t* scratch_dev, void* stream);
+int rch_staged_store(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev, int n_tiles,
+                     const int64_t* rows_dev, const void* product, int64_t product_stride, int channels, int head_dim,
+                     int out_dtype, int precision, const int32_t* scratch_dev, void* stream);
 
 /* ------------------------------------------------------------------------------------------
  * Fit side (reelcache/gpu_fitting.py, reelcache/factorization.py, reelcache/node_packets.py).

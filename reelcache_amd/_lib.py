@@ -16,7 +16,7 @@ import numpy as np
 from .errors import ConfigurationError, UnsupportedError
 
 LIBRARY = Path(__file__).resolve().with_name("libreelcache_hip.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # Status codes (RCH_E_*).
 OK, E_CONFIG, E_UNSUPPORTED, E_LAUNCH = 0, 1, 2, 3
@@ -78,6 +78,8 @@ _SIGNATURES = {
     "rch_restore_slice_blocks": ([_i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i)], _i),
     "rch_restore_sliced": ([_p, _i, _p, _i, _p, _i, _p, _i, _i, _i, _i, _i, _i, _i, _p, _p], _i),
     "rch_rope_store": ([_p, _i, _p, _i, _i, _i, _i, _p], _i),
+    "rch_staged_unpack": ([_p, _i, _p, _i, _p, _p, _i64, _i, _i, _i, _i, _p, _p], _i),
+    "rch_staged_store": ([_p, _i, _p, _i, _p, _p, _i64, _i, _i, _i, _i, _p, _p], _i),
     "rch_restore_noalloc": ([_p, _i, _p, _i, _p, _i, _p, _i, _i, _i, _i, _i, _i, _i, _i, _p], _i),
     "rch_fit_matrix_size": ([], _i),
     "rch_fit_absmax": ([_p, _i, _i, _i64, _i, _p], _i),

@@ -357,6 +357,118 @@ __global__ void __launch_bounds__(256) rope_store_kernel(const rch_job* __restri
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Staged comparison path: unpack -> library GEMM -> RoPE / cast / store
+// ---------------------------------------------------------------------------------------------
+
+// The coefficient prescale exponent of a job in the fp16 modes: the host's, or the one of the
+// device bound that rch_coefficient_bound left in its scratch word.
+__device__ __forceinline__ int staged_exponent(const rch_job* J, int precision, const int32_t* scratch) {
+    if (precision != RCH_PREC_FP16) return 0;
+    if (J->bound_index >= 0) return prescale_exponent(__int_as_float(scratch[J->bound_index]));
+    return static_cast<int>(J->coef_exp);
+}
+
+// One coefficient of token t, rank column k: dequantized with two roundings (uint8 rows,
+// pictures) or read as is (float sources), in fp32.
+template <int SRC>
+__device__ __forceinline__ float staged_coefficient(const rch_job* J, int64_t t, int k, const Coords& c) {
+    if constexpr (SRC == RCH_SRC_FLOAT) {
+        return load_value(J->src_ptr, t * J->src_row_stride + k * J->src_col_stride, static_cast<int>(J->src_dtype));
+    } else {
+        const uint32_t q = SRC == RCH_SRC_U8 ? gin<uint8_t>(J->src_ptr)[t * J->src_row_stride + k * J->src_col_stride]
+                                             : gin<uint8_t>(J->src_ptr)[picture_offset(J, k, c)];
+        return dequant(q, gin<float>(J->scale_ptr)[k], gin<float>(J->offset_ptr)[k]);
+    }
+}
+
+// Work rows [rows[job] + t] of the dense [rows, rank] coefficient matrix of one GEMM: 128 tokens x
+// 64 rank columns per workgroup, thread = (token, 4 consecutive columns), 8 tokens per thread.
+// fp16: times 2^e (exact), then one rounding to the work dtype, as the reference's unpack pass
+// (reelcache/restore_kernels.py:1518-1554).
+template <int SRC, int WORK>
+__global__ void __launch_bounds__(256) staged_unpack_kernel(const rch_job* __restrict__ jobs,
+                                                            const int32_t* __restrict__ tiles, int k_tiles,
+                                                            const int64_t* __restrict__ rows, int64_t work,
+                                                            int64_t work_stride, int precision,
+                                                            const int32_t* __restrict__ scratch) {
+    const int tile = blockIdx.x / k_tiles, kt = blockIdx.x - tile * k_tiles;
+    const int job = tiles[2 * tile];
+    const rch_job* J = jobs + job;
+    const int64_t t0 = tiles[2 * tile + 1];
+    const int rank = static_cast<int>(J->rank);
+    const int k0 = kt * 64 + (threadIdx.x & 15) * 4;
+    if (k0 >= rank) return;
+    const float pre = pow2f(staged_exponent(J, precision, scratch));
+    const int64_t first = rows[job];
+    for (int rep = 0; rep < 8; ++rep) {
+        const int64_t t = t0 + (threadIdx.x >> 4) + 16 * rep;
+        if (t >= J->tokens) break;
+        const Coords c = coords(J, static_cast<int>(t));
+        const int64_t at = (first + t) * work_stride;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int k = k0 + j;
+            if (k >= rank) break;
+            const float a = __fmul_rn(staged_coefficient<SRC>(J, t, k, c), pre);
+            if constexpr (WORK == RCH_DT_F32) gout<float>(work)[at + k] = a;
+            else if constexpr (WORK == RCH_DT_F16) gout<_Float16>(work)[at + k] = static_cast<_Float16>(a);
+            else gout<__bf16>(work)[at + k] = static_cast<__bf16>(a);
+        }
+    }
+}
+
+// fp32 product rows [rows[job] + t] -> times 2^-e (fp16) -> RoPE -> cast -> native store
+// (reelcache/restore_kernels.py:1557-1585 with PRESCALE).
+__global__ void __launch_bounds__(256) staged_store_kernel(const rch_job* __restrict__ jobs,
+                                                           const int32_t* __restrict__ tiles, int c_tiles,
+                                                           const int64_t* __restrict__ rows, int64_t product,
+                                                           int64_t product_stride, int channels, int head_dim,
+                                                           int out_dtype, int precision,
+                                                           const int32_t* __restrict__ scratch) {
+    const int tile = blockIdx.x / c_tiles, ct = blockIdx.x - tile * c_tiles;
+    const int job = tiles[2 * tile];
+    const rch_job* J = jobs + job;
+    const int64_t t0 = tiles[2 * tile + 1];
+    const int c0 = ct * 64 + (threadIdx.x & 3) * 16;
+    const int rope = static_cast<int>(J->rope);
+    const float inverse = pow2f(-staged_exponent(J, precision, scratch));
+    const int64_t first = rows[job];
+    for (int rep = 0; rep < 2; ++rep) {
+        const int64_t t = t0 + (threadIdx.x >> 2) + 64 * rep;
+        if (t >= J->tokens || c0 >= channels) continue;
+        const RCH_GLOBAL float* row = gin<float>(product) + (first + t) * product_stride;
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = c0 + i < channels ? __fmul_rn(row[c0 + i], inverse) : 0.0f;
+        if (rope != RCH_ROPE_NONE) {
+            const Coords c = coords(J, static_cast<int>(t));
+            apply_rope(J, rope, v, c0, channels, head_dim, t, c.f, c.y, c.x);
+        }
+        store16(J, v, c0, channels, head_dim, t, out_dtype);
+    }
+}
+
+template <int SRC>
+void launch_staged_unpack(int work_dtype, dim3 grid, hipStream_t s, const rch_job* jobs, const int32_t* tiles,
+                          int k_tiles, const int64_t* rows, int64_t work, int64_t work_stride, int precision,
+                          const int32_t* scratch) {
+    switch (work_dtype) {
+        case RCH_DT_F32:
+            hipLaunchKernelGGL((staged_unpack_kernel<SRC, RCH_DT_F32>), grid, dim3(256), 0, s, jobs, tiles, k_tiles,
+                               rows, work, work_stride, precision, scratch);
+            break;
+        case RCH_DT_F16:
+            hipLaunchKernelGGL((staged_unpack_kernel<SRC, RCH_DT_F16>), grid, dim3(256), 0, s, jobs, tiles, k_tiles,
+                               rows, work, work_stride, precision, scratch);
+            break;
+        default:
+            hipLaunchKernelGGL((staged_unpack_kernel<SRC, RCH_DT_BF16>), grid, dim3(256), 0, s, jobs, tiles, k_tiles,
+                               rows, work, work_stride, precision, scratch);
+            break;
+    }
+}
+
 bool valid_out(int out_dtype) {
     return out_dtype == RCH_DT_F32 || out_dtype == RCH_DT_F16 || out_dtype == RCH_DT_BF16;
 }
@@ -587,6 +699,60 @@ int rch_rope_store(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev
     hipLaunchKernelGGL(rope_store_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, as_stream(stream),
                        jobs_dev, tiles_dev, c_tiles, channels, head_dim, out_dtype);
     return check_launch("rch_rope_store");
+}
+
+int rch_staged_unpack(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev, int n_tiles,
+                      const int64_t* rows_dev, void* work, int64_t work_stride, int max_rank, int source_kind,
+                      int work_dtype, int precision, const int32_t* scratch_dev, void* stream) {
+    if (!jobs_dev || !tiles_dev || !rows_dev || !work || !scratch_dev || n_jobs <= 0 || n_tiles <= 0 ||
+        max_rank <= 0 || work_stride < max_rank)
+        return fail(RCH_E_CONFIG, "rch_staged_unpack: invalid launch arguments");
+    if (work_dtype != RCH_DT_F32 && work_dtype != RCH_DT_F16 && work_dtype != RCH_DT_BF16)
+        return fail(RCH_E_CONFIG, "rch_staged_unpack: work dtype must be f32, f16 or bf16");
+    if (precision != RCH_PREC_FP32 && precision != RCH_PREC_FP16 && precision != RCH_PREC_BF16)
+        return fail(RCH_E_UNSUPPORTED, "rch_staged_unpack: the staged path runs fp32, fp16 or bf16 (precision %d)",
+                    precision);
+    const int k_tiles = (max_rank + 63) / 64;
+    const int64_t blocks = static_cast<int64_t>(n_tiles) * k_tiles;
+    if (blocks > 0x7fffffff) return fail(RCH_E_CONFIG, "rch_staged_unpack: grid too large");
+    const dim3 grid(static_cast<unsigned>(blocks));
+    const int64_t address = reinterpret_cast<int64_t>(work);
+    hipStream_t s = as_stream(stream);
+    switch (source_kind) {
+        case RCH_SRC_FLOAT:
+            launch_staged_unpack<RCH_SRC_FLOAT>(work_dtype, grid, s, jobs_dev, tiles_dev, k_tiles, rows_dev, address,
+                                                work_stride, precision, scratch_dev);
+            break;
+        case RCH_SRC_U8:
+            launch_staged_unpack<RCH_SRC_U8>(work_dtype, grid, s, jobs_dev, tiles_dev, k_tiles, rows_dev, address,
+                                             work_stride, precision, scratch_dev);
+            break;
+        case RCH_SRC_PICTURE:
+            launch_staged_unpack<RCH_SRC_PICTURE>(work_dtype, grid, s, jobs_dev, tiles_dev, k_tiles, rows_dev, address,
+                                                  work_stride, precision, scratch_dev);
+            break;
+        default: return fail(RCH_E_CONFIG, "rch_staged_unpack: source kind %d is not a coefficient source", source_kind);
+    }
+    return check_launch("rch_staged_unpack");
+}
+
+int rch_staged_store(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev, int n_tiles,
+                     const int64_t* rows_dev, const void* product, int64_t product_stride, int channels, int head_dim,
+                     int out_dtype, int precision, const int32_t* scratch_dev, void* stream) {
+    if (!jobs_dev || !tiles_dev || !rows_dev || !product || !scratch_dev || n_jobs <= 0 || n_tiles <= 0 ||
+        channels <= 0 || head_dim <= 0 || head_dim % 2 || product_stride < channels)
+        return fail(RCH_E_CONFIG, "rch_staged_store: invalid launch arguments");
+    if (!valid_out(out_dtype)) return fail(RCH_E_CONFIG, "rch_staged_store: output dtype must be f32, f16 or bf16");
+    if (precision != RCH_PREC_FP32 && precision != RCH_PREC_FP16 && precision != RCH_PREC_BF16)
+        return fail(RCH_E_UNSUPPORTED, "rch_staged_store: the staged path runs fp32, fp16 or bf16 (precision %d)",
+                    precision);
+    const int c_tiles = (channels + 63) / 64;
+    const int64_t blocks = static_cast<int64_t>(n_tiles) * c_tiles;
+    if (blocks > 0x7fffffff) return fail(RCH_E_CONFIG, "rch_staged_store: grid too large");
+    hipLaunchKernelGGL(staged_store_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, as_stream(stream),
+                       jobs_dev, tiles_dev, c_tiles, rows_dev, reinterpret_cast<int64_t>(product), product_stride,
+                       channels, head_dim, out_dtype, precision, scratch_dev);
+    return check_launch("rch_staged_store");
 }
 
 }  // extern "C"

@@ -26,9 +26,14 @@ Backends (same names as the reference, reelcache/restore_kernels.py:138):
   launch group (gather/dequantize -> MFMA rank-view product -> RoPE -> cast ->
   strided store).  ``two_pass`` selects the same kernels (pictures are gathered
   inside the fused kernel; there is no separate unpack pass).
+* ``staged`` -- the comparison path of the reference's ``_staged_group``: a HIP
+  unpack of each GEMM group's coefficients into a dense work matrix, the GPU BLAS
+  library's product with FP32 output (``torch.mm``), then a HIP RoPE / cast /
+  store pass.  Precisions ``fp32``, ``fp16`` and ``bf16``; it follows the
+  process-wide torch matmul settings and refuses what they forbid.
 * ``reference`` -- plain torch, FP64 (default) or IEEE FP32, on the jobs' device.
-* ``staged`` and ``interpret`` (cuBLAS comparison and Triton interpreter in the
-  reference) do not exist on this platform and raise :class:`UnsupportedError`.
+* ``interpret`` (the Triton interpreter in the reference) has no counterpart and
+  raises :class:`UnsupportedError`.
 
 Precision modes keep the reference's names and error contract
 (:func:`error_bound`): ``fp32`` (FP32 matrix cores), ``fp16`` (prescaled
@@ -56,7 +61,8 @@ from .restore_handle import RestoreHandle, _sweep_deferred, park_failed, pending
 from .restore_model import (COEFFICIENT_DTYPES, LAYOUTS, OUTPUT_DTYPES, CoefficientSource, DenseSource, NativeView,
                             PictureSource, ReconstructionJob, RopePositions, RopeTable, expand_affine, wan_sections)
 from .restore_plan import (DEFAULT_MERGED, _DEFAULT_CONFIG, _RETIRED_SLABS, _STAGING, BASIS_DTYPES, SLICE_JOBS,  # noqa: F401
-                           SLICE_TOKENS, STREAM_TOKENS, TILE_TOKENS, _balanced_bounds, _capture_staging,
+                           SLICE_TOKENS, STAGED_PRECISIONS, STREAM_TOKENS, TILE_TOKENS, _balanced_bounds,
+                           _capture_staging, check_staged_precision, staged_gemm,
                            _coefficient_bound, _fast_flags, _pinned_bytes, _prescale_exponent,
                            _slice_heads, _slice_plan, _tiles, job_desc, reserve_capture_staging, run_call)
 from .restore_reference import (_OUTPUT_FLOOR, _UNIT_ROUNDOFF, _check_compute_dtype,  # noqa: F401
@@ -84,6 +90,11 @@ _REFERENCE_TILE_KEYS = {"BLOCK_M", "BLOCK_K", "num_warps", "num_stages", "N_GROU
                         "maxnreg", "_n_group"}
 
 
+# The reference's names for the staged GEMM and its settings check (restore_kernels.py:2153-2189).
+_staged_gemm = staged_gemm
+_check_staged_precision = check_staged_precision
+
+
 def device_config(device):
     """Launch configuration for a device (tile geometry of the HIP kernels)."""
     return dict(_DEFAULT_CONFIG)
@@ -98,9 +109,9 @@ def _resolve_backend(backend, cuda):
     """``backend`` resolved for jobs on a GPU (``cuda=True``) or host tensors; never a silent fallback."""
     if backend == "reference" or (backend == "auto" and not cuda):
         return "reference"
-    if backend in ("staged", "interpret"):
-        raise UnsupportedError(f"the {backend!r} backend (cuBLAS comparison / Triton interpreter) does not exist on "
-                               "ROCm; use 'fused' or 'reference'")
+    if backend == "interpret":
+        raise UnsupportedError("the 'interpret' backend (the Triton interpreter) does not exist on ROCm; use "
+                               "'fused', 'staged' or 'reference'")
     if not cuda:
         raise UnsupportedError(f"the {backend} backend needs GPU tensors; use 'reference'")
     reason = _lib.unavailable_reason()
@@ -109,7 +120,7 @@ def _resolve_backend(backend, cuda):
             raise UnsupportedError(f"backend='auto' cannot run the HIP reconstruction: {reason}. The FP64 reference "
                                    "is never substituted silently; pass backend='reference' to request it explicitly.")
         raise UnsupportedError(f"the {backend} backend is unavailable: {reason}")
-    return "fused"
+    return "staged" if backend == "staged" else "fused"
 
 
 def _resolve_precision(precision, device):
@@ -167,14 +178,16 @@ class _FusedCall:
     unrotated) and, with ``native_rope``, one for the pre-RoPE K that the engine's callable
     rotates before the copy into its slot."""
 
-    def __init__(self, device, stream, precision, config, keepalive, stage_events, stats):
+    def __init__(self, device, stream, precision, config, keepalive, stage_events, stats, staged=False):
         self.device, self.stream, self.precision = device, stream, precision
         self.config, self.keepalive, self.stage_events, self.stats = config, keepalive, stage_events, stats
+        self.staged = staged
         stats.update(grids=[], variants=[])
 
     def launch(self, jobs):
         launches, grids, variants = run_call([job_desc(job) for job in jobs], self.device, self.stream,
-                                             self.precision, self.config, self.keepalive, self.stage_events)
+                                             self.precision, self.config, self.keepalive, self.stage_events,
+                                             staged=self.staged)
         self.stats["launches"] += launches
         self.stats["grids"].extend(grids)
         self.stats["variants"].extend(variants)
@@ -219,7 +232,7 @@ def reconstruct(jobs, *, backend="auto", precision="auto", stream=None, wait_eve
     of the built-in rotation for jobs with RoPE.  ``config``: launch overrides
     (``workgroups_per_cu``, ``store_cost``, kernel-variant switches).  ``stage_events``: optional
     list receiving ``(stage, event)`` timing events ("start", "pack", "launch<n>" after the n-th
-    launch of the call, "fused", "rope_store").
+    launch of the call, "fused"; the staged backend adds "unpack", "gemm" and "rope_store").
 
     Returns a :class:`RestoreHandle`; destinations are valid after its event.
     """
@@ -236,6 +249,10 @@ def reconstruct(jobs, *, backend="auto", precision="auto", stream=None, wait_eve
     if resolved == "reference":
         _check_compute_dtype(compute_dtype, device)
         label = str(compute_dtype)
+    elif resolved == "staged":
+        # The staged GEMM follows process-wide torch settings: refuse before any work is enqueued.
+        precision = label = recommended_precision(device) if precision == "auto" else precision
+        check_staged_precision(precision)
     else:
         precision = label = _resolve_precision(precision, device)
     stream = _execution_stream(device, stream, wait_events)
@@ -246,7 +263,8 @@ def reconstruct(jobs, *, backend="auto", precision="auto", stream=None, wait_eve
             reconstruct_reference(jobs, compute_dtype=compute_dtype, native_rope=native_rope,
                                   native_rope_dtype=native_rope_dtype)
     else:
-        call = _FusedCall(device, stream, precision, _merged_config(config), keepalive, stage_events, stats)
+        call = _FusedCall(device, stream, precision, _merged_config(config), keepalive, stage_events, stats,
+                          staged=resolved == "staged")
         native = [job for job in jobs if native_rope is not None and job.rope is not None]
         fused = [job for job in jobs if native_rope is None or job.rope is None]
         try:

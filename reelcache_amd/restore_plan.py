@@ -28,6 +28,7 @@ import torch
 from . import _lib
 from .errors import ConfigurationError, UnsupportedError
 from .restore_model import CoefficientSource, DenseSource, PictureSource, settle_table_uploads
+from .restore_reference import _require_fp32_matmul
 
 TILE_TOKENS = 128  # tokens per workgroup tile (4 waves x 32)
 SLICE_TOKENS = 32  # tokens per tile of the channel-slice kernel (one wave's MFMA columns)
@@ -514,10 +515,11 @@ class _Layout:
     descriptor tables with buffer offsets where the call writes ``base + offset``;
     ``template`` is the host image of the buffer's tables, static parts filled."""
 
-    def __init__(self, descs, dynamic_flags, basis_groups, precision, config, device):
+    def __init__(self, descs, dynamic_flags, basis_groups, precision, config, device, staged=False):
         self.precision, self.config = precision, config
         self.code = _lib.PRECISION_CODES[precision]
-        self.static = bool(_config_value(config, "static_scratch"))
+        self.staged = staged
+        self.static = bool(_config_value(config, "static_scratch")) and not staged
         self.fp16_mode = precision in ("fp16", "fp16x2")
         self.grids, self.variants = [], []
         rows = np.stack([desc.row for desc in descs])
@@ -534,7 +536,9 @@ class _Layout:
                 at = arena.reserve(8 * len(desc.pictures))
                 self.picture_tables.append((index, at))
                 rows[index, _C_PIC_TABLE], relative[index, _C_PIC_TABLE] = at, 1
-        plans = self._launch_groups(descs, rows, arena, device)
+        self.staged_rows = np.zeros(len(descs), dtype=np.int64)
+        plans = self._launch_groups(descs, rows, arena, device, basis_groups)
+        self.staged_rows_offset = arena.add(self.staged_rows) if staged else None
         packs, pack_of = self._packs(descs, plans, basis_groups, arena)
         self._pack_layout(descs, rows, relative, plans, packs, pack_of)
         self.bound_tiles = _tiles(self.bound_jobs, descs) if self.bound_jobs else None
@@ -587,7 +591,7 @@ class _Layout:
             relative[index, _C_SCALE] = relative[index, _C_OFFSET] = 1
             first += size
 
-    def _launch_groups(self, descs, rows, arena, device):
+    def _launch_groups(self, descs, rows, arena, device, basis_groups):
         """Launch groups (source kind, dtypes, head geometry, rank class, straight-line eligibility)
         and the kernel variant, grid and work tables of each."""
         precision, config = self.precision, self.config
@@ -621,6 +625,9 @@ class _Layout:
             if kind == _lib.SRC_DENSE:
                 tiles = _tiles(members, descs)
                 plan.update(variant="dense", tiles=arena.add(tiles), n_tiles=len(tiles))
+                continue
+            if self.staged:
+                self._staged_plan(descs, plan, basis_groups, arena)
                 continue
             job_steps = {i: (descs[i].rank + 15) // 16 for i in members}
             max_ksteps = plan["max_ksteps"] = max(job_steps.values())
@@ -672,6 +679,25 @@ class _Layout:
             self.variants.append(plan["variant"])
         return plans
 
+    def _staged_plan(self, descs, plan, basis_groups, arena):
+        """GEMM groups of a staged launch group: jobs sharing a basis view and rank stack their
+        coefficient rows into one work matrix (job order), so each group is one library GEMM
+        (reelcache/restore_kernels.py:2198-2213)."""
+        gemms: dict = {}
+        for index in plan["members"]:
+            gemms.setdefault((basis_groups[index], descs[index].rank), []).append(index)
+        plan["gemms"] = []
+        for (_, rank), members in gemms.items():
+            first = 0
+            for index in members:
+                self.staged_rows[index] = first
+                first += descs[index].tokens
+            tiles = _tiles(members, descs)
+            plan["gemms"].append({"members": members, "rank": rank, "rows": first, "tiles": arena.add(tiles),
+                                  "n_tiles": len(tiles)})
+        plan.update(variant="staged", grid=0)
+        self.variants.append("staged")
+
     def _stream_plan(self, descs, plan, group_flags, compute_units, arena):
         """Work tables of a stream-kernel group: units (job, head, 32-token tile) job-major, and an
         equal split of them over the resident workgroups."""
@@ -701,7 +727,7 @@ class _Layout:
         pack_of: dict = {}
         by_basis: dict = {}
         for plan in plans:
-            if plan["variant"] == "dense":
+            if plan["variant"] in ("dense", "staged"):
                 continue
             used = []
             for index in plan["members"]:
@@ -828,10 +854,10 @@ class _Layout:
             buffer[start:start + 4 * len(self.bound_jobs)].zero_()  # fill kernel, not a memset (graph-capture safe)
         buffer[:image.size].copy_(host, non_blocking=True)
         keepalive.extend((host, buffer))
-        return self._launch(base, scratch_base, packs, stream, stage_events)
+        return self._launch(base, scratch_base, packs, stream, stage_events, descs, keepalive)
 
 
-    def _launch(self, base, scratch_base, packs, stream, stage_events):
+    def _launch(self, base, scratch_base, packs, stream, stage_events, descs, keepalive):
         hip_stream = stream.cuda_stream
         jobs, table = self.jobs, base + self.desc_offset
         launches = 0
@@ -849,6 +875,9 @@ class _Layout:
             launches += 1
         for plan in self.plans:
             variant = plan["variant"]
+            if variant == "staged":
+                launches += self._launch_staged(plan, base, scratch_base, stream, stage_events, descs, keepalive)
+                continue
             if variant == "dense":
                 _lib.call("rch_rope_store", table, jobs, base + plan["tiles"], plan["n_tiles"], plan["channels"],
                           plan["head_dim"], plan["out_dtype"], hip_stream)
@@ -871,6 +900,80 @@ class _Layout:
         if stage_events is not None:
             stage_events.append(("fused", _record(stream)))
         return launches
+
+    def _launch_staged(self, plan, base, scratch_base, stream, stage_events, descs, keepalive):
+        """The staged comparison path of one launch group: every GEMM group's unpack, then the
+        library GEMMs (FP32 output), then the RoPE / cast / store launches, with the reference's
+        stage events ("unpack", "gemm", "rope_store")."""
+        hip_stream = stream.cuda_stream
+        table, jobs, rows = base + self.desc_offset, self.jobs, base + self.staged_rows_offset
+        work_dtype = _STAGED_WORK[self.precision]
+        launches, products = 0, []
+        for gemm in plan["gemms"]:
+            work = torch.empty((gemm["rows"], gemm["rank"]), dtype=work_dtype, device=descs[0].dst.device)
+            keepalive.append(work)
+            _lib.call("rch_staged_unpack", table, jobs, base + gemm["tiles"], gemm["n_tiles"], rows, work.data_ptr(),
+                      work.stride(0), gemm["rank"], plan["kind"], _DTYPE_CODES[work_dtype], self.code, scratch_base,
+                      hip_stream)
+            launches += 1
+            products.append(work)
+        if stage_events is not None:
+            stage_events.append(("unpack", _record(stream)))
+        for position, gemm in enumerate(plan["gemms"]):
+            basis = descs[gemm["members"][0]].basis[:gemm["rank"]]
+            products[position] = staged_gemm(products[position], basis, self.precision)
+            keepalive.append(products[position])
+            launches += 1
+        if stage_events is not None:
+            stage_events.append(("gemm", _record(stream)))
+        for gemm, product in zip(plan["gemms"], products):
+            _lib.call("rch_staged_store", table, jobs, base + gemm["tiles"], gemm["n_tiles"], rows, product.data_ptr(),
+                      product.stride(0), plan["channels"], plan["head_dim"], plan["out_dtype"], self.code, scratch_base,
+                      hip_stream)
+            launches += 1
+        if stage_events is not None:
+            stage_events.append(("rope_store", _record(stream)))
+        return launches
+
+
+# Work (coefficient) dtype of the staged path's GEMM per precision.
+_STAGED_WORK = {"fp32": torch.float32, "fp16": torch.float16, "bf16": torch.bfloat16}
+STAGED_PRECISIONS = ("fp32", "tf32", "fp16", "bf16")
+
+
+def check_staged_precision(precision):
+    """The staged GEMM's precision follows process-wide torch settings: check them, never change
+    them (reelcache/restore_kernels.py:2153-2164).  gfx950 has no TF32 matrix cores, so ``tf32``
+    is refused as in the fused path."""
+    if precision not in STAGED_PRECISIONS:
+        raise UnsupportedError("the staged backend supports fp32, tf32, fp16 and bf16")
+    if precision == "tf32":
+        raise UnsupportedError("the staged tf32 GEMM has no matrix-core form on gfx950 (no TF32 MFMA); use fp32, "
+                               "fp16 or bf16")
+    if precision == "fp32":
+        _require_fp32_matmul("cuda", ("ieee",), "the staged fp32 GEMM (rocBLAS)")
+    elif precision == "fp16" and getattr(torch.backends.cuda.matmul, "allow_fp16_accumulation", False):
+        raise UnsupportedError(
+            "the staged fp16 GEMM needs FP32 accumulation, but this process allows FP16 accumulation in the BLAS "
+            "library (torch.backends.cuda.matmul.allow_fp16_accumulation=True). That setting is process-wide, so "
+            "restore_kernels never changes it: use the fused backend or change the setting in your own code.")
+
+
+def staged_gemm(coefficients, basis, precision):
+    """Rank-view product with FP32 accumulation and FP32 output on the GPU BLAS library
+    (reelcache/restore_kernels.py:2167-2189): ``torch.mm`` on FP32 operands for fp32; FP16 / BF16
+    operands through ``torch.mm(..., out_dtype=torch.float32)``.  A Torch that rejects that
+    overload raises :class:`UnsupportedError` (no retry with a 16-bit output, which would round and
+    could overflow the prescaled products); every other error propagates unchanged."""
+    if precision == "fp32":
+        return torch.mm(coefficients, basis.float())
+    operand = basis.to(_STAGED_WORK[precision])
+    try:
+        return torch.mm(coefficients, operand, out_dtype=torch.float32)
+    except (TypeError, NotImplementedError) as error:
+        raise UnsupportedError(
+            f"the staged {precision} GEMM needs torch.mm(..., out_dtype=torch.float32) (FP32 output); "
+            f"Torch {torch.__version__} rejected it: {type(error).__name__}: {error}") from error
 
 
 _LAYOUTS: dict = {}
@@ -895,9 +998,10 @@ def _pinned_host(nbytes):
     return torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
 
 
-def run_call(descs, device, stream, precision, config, keepalive, stage_events=None):
+def run_call(descs, device, stream, precision, config, keepalive, stage_events=None, staged=False):
     """Plan (or reuse the layout of) one HIP call and enqueue it on ``stream``; returns
-    ``(launches, grids, variants)``."""
+    ``(launches, grids, variants)``.  ``staged``: the staged comparison path (unpack, library
+    GEMM, store) for the factorized jobs instead of the fused kernels."""
     dst = [desc.dst.data_ptr() + desc.dst_shift for desc in descs]
     src = [desc.source_address() for desc in descs]
     dynamic = [(_lib.JF_DST_VEC if desc.dst_vec_rule and not d & 15 else 0)
@@ -909,10 +1013,11 @@ def run_call(descs, device, stream, precision, config, keepalive, stage_events=N
         if desc.basis is not None:
             bases[index] = address = desc.basis.data_ptr()
             groups[index] = first_of.setdefault((address, desc.basis_key), index)
-    key = (precision, _config_key(config), tuple(desc.key_id for desc in descs), tuple(dynamic), tuple(groups))
+    key = (precision, _config_key(config), tuple(desc.key_id for desc in descs), tuple(dynamic), tuple(groups),
+           staged)
     layout = _LAYOUTS.get(key)
     if layout is None:
-        layout = _Layout(descs, dynamic, groups, precision, config, device)
+        layout = _Layout(descs, dynamic, groups, precision, config, device, staged)
         if len(_LAYOUTS) >= _LAYOUT_LIMIT:
             _LAYOUTS.clear()
         _LAYOUTS[key] = layout
