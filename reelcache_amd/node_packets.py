@@ -35,7 +35,8 @@ from .quantize import (MAX_DIMENSION, PIXEL_FORMATS, affine_from_extrema, coveri
 from .types import EncodedTensor, MatrixKey, TensorContext, json_copy
 
 __all__ = ["CANVAS_ALIGNMENT", "CANVAS_RANK_LADDER", "FACTOR_PACK_SCHEMA", "MIN_CANVAS", "PACK_SCHEMA",
-           "affine_from_extrema", "attach_pack_bases", "canonical_canvas", "canvas_ladder", "detach_pack_bases",
+           "affine_from_extrema", "attach_pack_bases", "canonical_canvas", "canonical_canvas_shapes", "canvas_ladder",
+           "detach_pack_bases",
            "mosaic_device", "pack_tile_index", "quantize_device", "quantize_many", "quantize_with_extrema",
            "video_layout"]
 
@@ -122,6 +123,29 @@ def canonical_canvas(frames: int, height: int, width: int, pix_fmt: str, node_ma
             return {"width": canvas_width, "height": canvas_height, "rank_step": step,
                     "policy": "canonical_rank_ladder"}
     raise ConfigurationError("canvas ladder does not cover the node rank")
+
+
+def canonical_canvas_shapes(frames: int, height: int, width: int, pix_fmt: str, *, channels: int,
+                            max_rank: int | None = None,
+                            ladder: Sequence[int] | None = None) -> list[tuple[int, int, str]]:
+    """``(width, height, pix_fmt)`` of every canonical node canvas of one tile geometry, smallest
+    first (reelcache/packed_decode.py:115-139): the distinct canvases of :func:`canvas_ladder` over
+    all ``channels`` ranks, up to the first step covering ``max_rank`` (default: every rank), without
+    those beyond the maximum picture dimension (no pack can use them).  These are the pictures a
+    decoder must be ready for to restore any node pack of the geometry."""
+    need(type(channels) is int and channels >= 1, "channels must be a positive integer")
+    limit = channels if max_rank is None else max_rank
+    need(type(limit) is int and 1 <= limit <= channels, "max_rank must be an integer in [1, channels]")
+    need(pix_fmt in PIXEL_FORMATS, f"HEVC supports exactly {PIXEL_FORMATS}, not {pix_fmt!r}", UnsupportedError)
+    shapes: list[tuple[int, int, str]] = []
+    for step, canvas_width, canvas_height in canvas_ladder(frames, height, width, pix_fmt, max_rank=channels,
+                                                           ladder=CANVAS_RANK_LADDER if ladder is None else ladder):
+        shape = (canvas_width, canvas_height, pix_fmt)
+        if max(canvas_width, canvas_height) <= MAX_DIMENSION and shape not in shapes:
+            shapes.append(shape)
+        if step >= limit:
+            break
+    return shapes
 
 
 def _check(coefficients) -> None:

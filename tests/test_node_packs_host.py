@@ -20,7 +20,7 @@ import torch
 
 from reelcache_amd import node_packets as npk
 from reelcache_amd import quantize as pq
-from reelcache_amd.errors import ConfigurationError, IntegrityError
+from reelcache_amd.errors import ConfigurationError, IntegrityError, UnsupportedError
 from reelcache_amd.types import EncodedTensor, MatrixKey, ModelIdentity, TensorContext
 
 
@@ -96,6 +96,29 @@ def _pack(rng):
         bases.append(raw)
     metadata = {"schema": npk.PACK_SCHEMA, "tiles": tiles, "payloads": descriptors}
     return EncodedTensor(metadata, payloads), bases
+
+
+def test_canonical_canvas_shapes_known_answers():
+    """The reference's known answers (tests/test_packed_nvdec.py:1404-1424): the shapes are the
+    ladder's canvases in order; every rank's canonical canvas is one of them and is the last shape
+    when ``max_rank`` is that rank; the CausVid geometry has 15 canonical canvases, 9 up to rank
+    384; bad ranks and pixel formats are refused."""
+    for frames, height, width, channels in ((3, 30, 52, 1536), (8, 22, 40, 3072), (4, 44, 82, 4096)):
+        shapes = npk.canonical_canvas_shapes(frames, height, width, "yuv444p", channels=channels)
+        ladder = npk.canvas_ladder(frames, height, width, "yuv444p", max_rank=channels)
+        assert shapes == [(w, h, "yuv444p") for _, w, h in ladder]
+        for rank in range(1, channels + 1, 7):
+            canvas = npk.canonical_canvas(frames, height, width, "yuv444p", rank, channels=channels)
+            assert (canvas["width"], canvas["height"], "yuv444p") in shapes
+            bounded = npk.canonical_canvas_shapes(frames, height, width, "yuv444p", channels=channels, max_rank=rank)
+            assert bounded[-1] == (canvas["width"], canvas["height"], "yuv444p")
+    assert len(npk.canonical_canvas_shapes(3, 30, 52, "yuv444p", channels=1536)) == 15  # CausVid
+    assert len(npk.canonical_canvas_shapes(3, 30, 52, "yuv444p", channels=1536, max_rank=384)) == 9
+    for bad in (0, 1537, 2.0):
+        with pytest.raises(ConfigurationError):
+            npk.canonical_canvas_shapes(3, 30, 52, "yuv444p", channels=1536, max_rank=bad)
+    with pytest.raises(UnsupportedError):
+        npk.canonical_canvas_shapes(3, 30, 52, "rgb24", channels=1536)
 
 
 def test_pack_bases_detach_and_attach_byte_exact():
