@@ -156,6 +156,38 @@ def test_causvid_layer_full_size(device):
         assert float((np.abs(out[sample] - exact) - bound).max()) <= 0
 
 
+def test_causvid_full_jobs_in_a_bf16_cache(device):
+    """One full CausVid K job (rank 128, Wan RoPE) and one full V job (rank 192) of a layer call
+    into a bf16 cache, checked on every token: each element within the oracle's fp16x2 bound and
+    each slot within rel-Frobenius 1e-3 of the oracle's reconstruction cast to bf16."""
+    rng = np.random.default_rng(29)
+    heads, head_dim, grid = 12, 128, (3, 30, 52)
+    tokens = 4680
+    table = rk.RopeTable.from_complex(torch.from_numpy(orc.wan_freqs(head_dim, 64)))
+    bases = [torch.from_numpy(np.linalg.qr(rng.standard_normal((1536, rows)))[0].T.copy()).to(torch.bfloat16)
+             .to(device) for rows in (128, 192)]
+    cache_k = destination("BTHD", 7 * tokens, heads, head_dim, "bfloat16", device)
+    cache_v = destination("BTHD", 7 * tokens, heads, head_dim, "bfloat16", device)
+    cases = []
+    for chunk in range(7):
+        cases.append(make_case(rng, grid=grid, heads=heads, head_dim=head_dim, rank=128,
+                               view=rk.NativeView(cache_k, token_offset=chunk * tokens), basis=bases[0], table=table,
+                               rope_rows=(3 * chunk, 0, 0), out_dtype="bfloat16", device=device))
+        cases.append(make_case(rng, grid=grid, heads=heads, head_dim=head_dim, rank=192,
+                               view=rk.NativeView(cache_v, token_offset=chunk * tokens), basis=bases[1], rope="none",
+                               out_dtype="bfloat16", device=device))
+    handle = rk.reconstruct([case.job for case in cases])
+    handle.release()
+    assert set(handle.stats["variants"]) == {"pairs"}, handle.stats["variants"]
+    for case in (cases[6], cases[11]):  # the K job of chunk 3, the V job of chunk 5
+        values, bound = expected(case, "fp16x2")
+        out = written(case)
+        excess = np.abs(out - values) - bound
+        assert float(excess.max()) <= 0, f"{int((excess > 0).sum())} of {excess.size} elements exceed the bound"
+        cast = torch.from_numpy(values).float().to(torch.bfloat16).double().numpy()
+        assert orc.relative_frobenius(out, cast) <= 1e-3
+
+
 def test_empty_call_and_errors(device):
     handle = rk.reconstruct([], backend="auto")
     assert handle.query() and handle.event is None
