@@ -260,6 +260,20 @@ def fit_workload(device, seed=2, distinct=60):
     return sources, contexts
 
 
+def _consecutive_host_rows(host_rows):
+    """The flat pinned buffer that holds ``host_rows`` back to back in this order, or None."""
+    first = host_rows[0]
+    base = first._base
+    if base is None or not base.is_pinned() or base.dim() != 1:
+        return None
+    offset = first.storage_offset()
+    for rows in host_rows:
+        if rows._base is not base or not rows.is_contiguous() or rows.storage_offset() != offset:
+            return None
+        offset += rows.numel()
+    return base[first.storage_offset() - base.storage_offset():offset - base.storage_offset()]
+
+
 def fit_step(sources, contexts, device):
     """One chunk: plan every matrix, then finalize it on its planned rows (projection, stored and
     span energies, codes; device)."""
@@ -278,9 +292,12 @@ def fit_step(sources, contexts, device):
     planned = time.perf_counter()
     # Final measurement on the planned FP16 rank views: projection, stored and span energies,
     # condition bound and 8-bit codes of all 60 matrices in batched launches.
-    # The planned rows (host, one block per matrix) go to the device in one pinned transfer.
+    # The planned rows (host, one block per matrix) go to the device in one asynchronous copy: the
+    # planner leaves them as consecutive views of one pinned buffer (gathered otherwise).
     host_rows = [plan.plans[k].new_rows for k in keys]
-    staged = torch.cat([rows.reshape(-1) for rows in host_rows]).pin_memory()
+    staged = _consecutive_host_rows(host_rows)
+    if staged is None:
+        staged = torch.cat([rows.reshape(-1) for rows in host_rows]).pin_memory()
     device_rows = staged.to(device, non_blocking=True)
     items, offset = [], 0
     for k, host in zip(keys, host_rows):

@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-#define RCH_ABI_VERSION 9
+#define RCH_ABI_VERSION 10
 
 /* Status codes (mapped to reelcache errors by the host). */
 #define RCH_OK 0
@@ -429,6 +429,26 @@ typedef struct rch_quantize_job {
  * coefficients of every matrix of a chunk after projection.
  */
 int rch_quantize_batched(const rch_quantize_job* jobs_dev, int n_jobs, int64_t max_rows, void* stream);
+
+/* One block of seeded standard normals: fp32 dst[r * stride + c] for r < rows, c < cols. */
+typedef struct rch_gauss_job {
+    int64_t dst_ptr;
+    int64_t rows;
+    int64_t cols;
+    int64_t stride;       /* elements between rows */
+    int64_t seed;         /* 64-bit Philox-4x32-10 key */
+    int64_t reserved[3];
+} rch_gauss_job;          /* 8 x int64 = 64 bytes */
+
+/*
+ * Seeded Gaussian blocks of many matrices in one launch (grid: 1024-element groups x jobs):
+ * element e = r * cols + c of a job is the (e % 4)-th normal of counter e / 4 (Philox-4x32-10
+ * under the job's key, then Box-Muller), so a block's values depend only on its seed and shape.
+ * max_elements = the largest rows * cols.  Replaces the per-matrix seeded torch generators of the
+ * start blocks of gram / top-k directions and anchor sketches (reelcache/rank_method.py:479-484,
+ * :591-631); the start columns only steer the solvers (every rank is verified on stored factors).
+ */
+int rch_fit_gaussian(const rch_gauss_job* jobs_dev, int n_jobs, int64_t max_elements, void* stream);
 
 /*
  * Batched upper Cholesky factor and its inverse, in FP64: for each of n symmetric positive

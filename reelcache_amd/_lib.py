@@ -16,7 +16,7 @@ import numpy as np
 from .errors import ConfigurationError, UnsupportedError
 
 LIBRARY = Path(__file__).resolve().with_name("libreelcache_hip.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 # Status codes (RCH_E_*).
 OK, E_CONFIG, E_UNSUPPORTED, E_LAUNCH = 0, 1, 2, 3
@@ -59,6 +59,8 @@ FIT_FIELDS = ("src_ptr", "src_dtype", "rows", "src_stride", "basis_ptr", "basis_
 FIT_DTYPE = np.dtype([(name, "<i8") for name in FIT_FIELDS])
 QUANTIZE_FIELDS = ("values_ptr", "rows", "cols", "stride", "affine_ptr", "codes_ptr", "code_stride", "reserved")
 QUANTIZE_DTYPE = np.dtype([(name, "<i8") for name in QUANTIZE_FIELDS])
+GAUSS_FIELDS = ("dst_ptr", "rows", "cols", "stride", "seed", "reserved0", "reserved1", "reserved2")
+GAUSS_DTYPE = np.dtype([(name, "<i8") for name in GAUSS_FIELDS])
 # rch_slice_entry field order (8 x int32).
 SLICE_ENTRY_FIELDS = ("tile0", "head0", "nh", "u0", "u1", "pack_job", "pack_ksteps", "reserved")
 SLICE_ENTRY_DTYPE = np.dtype([(name, "<i4") for name in SLICE_ENTRY_FIELDS])
@@ -90,6 +92,7 @@ _SIGNATURES = {
     "rch_quantize": ([_p, _i64, _i, _i64, _p, _p, _p, _i64, _p], _i),
     "rch_quantize_batched": ([_p, _i, _i64, _p], _i),
     "rch_cholesky_inverse": ([_p, _p, _p, _i, _i, _p], _i),
+    "rch_fit_gaussian": ([_p, _i, _i64, _p], _i),
 }
 # Further entry points registered by other modules are bound when present.
 _OPTIONAL_SIGNATURES: dict = {}

@@ -387,6 +387,69 @@ __global__ void __launch_bounds__(kThreads) project_kernel(const rch_fit_matrix*
     }
 }
 
+// The 4 channels of tokens g + 4v (v = 0..3) of a lane's 64-channel group, as raw 16-bit pairs
+// (or fp32 words), loaded ahead of their use.
+template <int DT>
+struct SourceQuad {
+    using word = std::conditional_t<DT == RCH_DT_F32, u4, u2>;
+    word w[4];
+};
+
+template <int DT>
+__device__ __forceinline__ void load_quad(__amdgpu_buffer_rsrc_t xs, const rch_fit_matrix* M, int c, bool c_ok,
+                                          SourceQuad<DT>& q) {
+    constexpr int E = esize<DT>();
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int token = (threadIdx.x & 63) / 16 + 4 * v;
+        const uint32_t offset = c_ok ? static_cast<uint32_t>((token * M->src_stride + c) * E) : kOutOfRange;
+        if constexpr (DT == RCH_DT_F32) {
+            q.w[v] = __builtin_amdgcn_raw_buffer_load_b128(xs, offset, 0, 0);
+        } else {
+            q.w[v] = __builtin_amdgcn_raw_buffer_load_b64(xs, offset, 0, 0);
+        }
+    }
+}
+
+// Residual of one 64-channel group: e = x - r per element, FP64 sums of x^2 and e^2, optional fp32 store.
+template <int DT>
+__device__ __forceinline__ void residual_group(const SourceQuad<DT>& q, const d4 (&acc)[4], int c, bool c_ok,
+                                               int64_t wt, int64_t left, int channels, RCH_GLOBAL float* resid,
+                                               double& src, double& err) {
+    const int g = (threadIdx.x & 63) >> 4;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int token = g + 4 * v;
+        double a[4];
+        if constexpr (DT == RCH_DT_F32) {
+#pragma unroll
+            for (int b = 0; b < 4; ++b) a[b] = static_cast<double>(__uint_as_float(q.w[v][b]));
+        } else {
+#pragma unroll
+            for (int b = 0; b < 4; ++b) a[b] = static_cast<double>(half_bits<DT>((q.w[v][b >> 1] >> (16 * (b & 1))) & 0xffffu));
+        }
+        double e[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            e[b] = a[b] - acc[b][v];
+            // The scale s is applied once per tile: sum (a / s)^2 = (sum a^2) / s^2 up to the rounding
+            // of the FP64 sums (relative 1e-16), without two FP64 divisions per element.
+            src += a[b] * a[b];
+            err += e[b] * e[b];
+        }
+        if (resid && c_ok && token < left) {
+            const f4 out = {static_cast<float>(e[0]), static_cast<float>(e[1]), static_cast<float>(e[2]),
+                            static_cast<float>(e[3])};
+            *reinterpret_cast<RCH_GLOBAL f4*>(resid + (wt + token) * channels + c) = out;
+        }
+    }
+}
+
+// The four B operands (channels 4i .. 4i + 3 of basis row k) from one 8-byte load, as doubles.
+__device__ __forceinline__ double basis_operand(const u2& w, int b) {
+    return static_cast<double>(half_bits<RCH_DT_F16>((w[b >> 1] >> (16 * (b & 1))) & 0xffffu));
+}
+
 // ---------------------------------------------------------------------------------------------
 // Residual energies on v_mfma_f64_16x16x4f64: D[m = token][n = channel] = sum_k P[token][k] Q[k][c].
 // Workgroup = 64-token tile of one matrix, wave w = tokens 16w .. 16w + 15, looping over
@@ -394,9 +457,14 @@ __global__ void __launch_bounds__(kThreads) project_kernel(const rch_fit_matrix*
 // block b is channel 4i + b of the group, so after the four blocks lane l (i = l % 16,
 // g = l / 16) holds channels 4i .. 4i + 3 of tokens g + 4v (v = 0..3, the f64 accumulator's row
 // (l / 16) + 4v): X and the residual move as 4-channel vectors, 16 lanes covering 64 contiguous
-// channels of a row.  Per 16-rank step a lane loads P[token i][4g .. 4g + 3] (one 16-byte load,
-// the A operand; MFMA step j takes rank 4g + j) and, for each j, Q[4g + j][4i .. 4i + 3] (one
-// 8-byte load: the B operands of the four blocks).
+// channels of a row.  Per 16-rank step a lane takes P[token i][4g .. 4g + 3] (the A operand; MFMA
+// step j takes rank 4g + j) and, for each j, Q[4g + j][4i .. 4i + 3] (one 8-byte load: the B
+// operands of the four blocks).
+//
+// Ranks up to 64 (the common fit ranks) keep the wave's P block in registers for the whole
+// channel loop (loaded once instead of once per channel group) and load a group's source
+// elements before its MFMAs; larger ranks stream P per step.  Both paths add the products in the same
+// order (rank ascending within each block), so their results are identical.
 // ---------------------------------------------------------------------------------------------
 
 template <int DT>
@@ -406,7 +474,6 @@ __global__ void __launch_bounds__(kThreads) residual_kernel(const rch_fit_matrix
     const int rank = static_cast<int>(M->rank);
     const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 64;
     if (t0 >= rows) return;
-    constexpr int E = esize<DT>();
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int g = lane >> 4, i16 = lane & 15;
     const int64_t wt = t0 + 16 * wave;
@@ -423,60 +490,70 @@ __global__ void __launch_bounds__(kThreads) residual_kernel(const rch_fit_matrix
     RCH_GLOBAL float* resid = M->resid_ptr ? gout<float>(M->resid_ptr) : nullptr;
 
     double src = 0.0, err = 0.0;
-    for (int c64 = 0; c64 < channels; c64 += 64) {
-        const int c = c64 + 4 * i16;  // this lane's 4 channels (channels % 8 == 0: all or none in range)
-        const bool c_ok = c < channels;
-        d4 acc[4] = {d4{}, d4{}, d4{}, d4{}};
-        for (int k0 = 0; k0 < rank; k0 += 16) {
-            const int k = k0 + 4 * g;
-            const u4 pw = __builtin_amdgcn_raw_buffer_load_b128(ps, k < rank ? p_row + static_cast<uint32_t>(k * 4) : kOutOfRange,
-                                                                0, 0);
-            u2 qw[4];
+    if (rank <= 64) {
+        const int steps = (rank + 15) >> 4;  // uniform
+        u4 pw[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t q_off = (k + j < rank && c_ok) ? static_cast<uint32_t>(k + j) * q_stride + 2u * c : kOutOfRange;
-                qw[j] = __builtin_amdgcn_raw_buffer_load_b64(qs, q_off, 0, 0);
-            }
+        for (int t = 0; t < 4; ++t) {
+            const int k = 16 * t + 4 * g;
+            pw[t] = __builtin_amdgcn_raw_buffer_load_b128(ps, (t < steps && k < rank) ? p_row + static_cast<uint32_t>(k * 4)
+                                                                                     : kOutOfRange, 0, 0);
+        }
+        for (int c64 = 0; c64 < channels; c64 += 64) {
+            const int c = c64 + 4 * i16;  // this lane's 4 channels (channels % 8 == 0: all or none in range)
+            const bool c_ok = c < channels;
+            SourceQuad<DT> xq;
+            load_quad<DT>(xs, M, c, c_ok, xq);
+            d4 acc[4] = {d4{}, d4{}, d4{}, d4{}};
+#pragma unroll 1
+            for (int t = 0; t < steps; ++t) {
+                const int k = 16 * t + 4 * g;
+                u2 qw[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                // P rows may hold padding beyond the rank; its basis rows read as zero.
-                const double pa = k + j < rank ? static_cast<double>(__uint_as_float(pw[j])) : 0.0;
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t q_off =
+                        (k + j < rank && c_ok) ? static_cast<uint32_t>(k + j) * q_stride + 2u * c : kOutOfRange;
+                    qw[j] = __builtin_amdgcn_raw_buffer_load_b64(qs, q_off, 0, 0);
+                }
+                const u4 p = t == 0 ? pw[0] : t == 1 ? pw[1] : t == 2 ? pw[2] : pw[3];
 #pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                    const uint32_t half = (qw[j][b >> 1] >> (16 * (b & 1))) & 0xffffu;
-                    const double qb = static_cast<double>(half_bits<RCH_DT_F16>(half));
-                    acc[b] = __builtin_amdgcn_mfma_f64_16x16x4f64(pa, qb, acc[b], 0, 0, 0);
+                for (int j = 0; j < 4; ++j) {
+                    // P rows may hold padding beyond the rank; its basis rows read as zero.
+                    const double pa = k + j < rank ? static_cast<double>(__uint_as_float(p[j])) : 0.0;
+#pragma unroll
+                    for (int b = 0; b < 4; ++b)
+                        acc[b] = __builtin_amdgcn_mfma_f64_16x16x4f64(pa, basis_operand(qw[j], b), acc[b], 0, 0, 0);
                 }
             }
+            residual_group<DT>(xq, acc, c, c_ok, wt, left, channels, resid, src, err);
         }
+    } else {
+        for (int c64 = 0; c64 < channels; c64 += 64) {
+            const int c = c64 + 4 * i16;
+            const bool c_ok = c < channels;
+            d4 acc[4] = {d4{}, d4{}, d4{}, d4{}};
+            for (int k0 = 0; k0 < rank; k0 += 16) {
+                const int k = k0 + 4 * g;
+                const u4 pw = __builtin_amdgcn_raw_buffer_load_b128(
+                    ps, k < rank ? p_row + static_cast<uint32_t>(k * 4) : kOutOfRange, 0, 0);
+                u2 qw[4];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int token = g + 4 * v;
-            const uint32_t offset = c_ok ? static_cast<uint32_t>((token * M->src_stride + c) * E) : kOutOfRange;
-            double a[4];
-            if constexpr (DT == RCH_DT_F32) {
-                const u4 w = __builtin_amdgcn_raw_buffer_load_b128(xs, offset, 0, 0);
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t q_off =
+                        (k + j < rank && c_ok) ? static_cast<uint32_t>(k + j) * q_stride + 2u * c : kOutOfRange;
+                    qw[j] = __builtin_amdgcn_raw_buffer_load_b64(qs, q_off, 0, 0);
+                }
 #pragma unroll
-                for (int b = 0; b < 4; ++b) a[b] = static_cast<double>(__uint_as_float(w[b]));
-            } else {
-                const u2 w = __builtin_amdgcn_raw_buffer_load_b64(xs, offset, 0, 0);
+                for (int j = 0; j < 4; ++j) {
+                    const double pa = k + j < rank ? static_cast<double>(__uint_as_float(pw[j])) : 0.0;
 #pragma unroll
-                for (int b = 0; b < 4; ++b) a[b] = static_cast<double>(half_bits<DT>((w[b >> 1] >> (16 * (b & 1))) & 0xffffu));
+                    for (int b = 0; b < 4; ++b)
+                        acc[b] = __builtin_amdgcn_mfma_f64_16x16x4f64(pa, basis_operand(qw[j], b), acc[b], 0, 0, 0);
+                }
             }
-            double e[4];
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                e[b] = a[b] - acc[b][v];
-                // The scale s is applied once per tile below: sum (a / s)^2 = (sum a^2) / s^2 up to
-                // the rounding of the FP64 sums (relative 1e-16), without two FP64 divisions per element.
-                src += a[b] * a[b];
-                err += e[b] * e[b];
-            }
-            if (resid && c_ok && token < left) {
-                const f4 out = {static_cast<float>(e[0]), static_cast<float>(e[1]), static_cast<float>(e[2]),
-                                static_cast<float>(e[3])};
-                *reinterpret_cast<RCH_GLOBAL f4*>(resid + (wt + token) * channels + c) = out;
-            }
+            SourceQuad<DT> xq;
+            load_quad<DT>(xs, M, c, c_ok, xq);
+            residual_group<DT>(xq, acc, c, c_ok, wt, left, channels, resid, src, err);
         }
     }
     // Fixed-order reduction: butterfly within the wave, then waves 0..3 in order.
@@ -653,6 +730,59 @@ __global__ void __launch_bounds__(kCholThreads) cholesky_inverse_kernel(const do
     if (tid == 0) info[blockIdx.x] = 0;
 }
 
+// ---------------------------------------------------------------------------------------------
+// Seeded Gaussian columns (start blocks of the subspace solvers)
+//
+// Counter-based Philox-4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy as
+// 1, 2, 3", SC 2011): the key is the job's 64-bit seed, the counter the index of a group of four
+// elements, so every element has a fixed value whatever the launch shape.  Box-Muller turns each
+// pair of 32-bit words into two standard normals.
+// ---------------------------------------------------------------------------------------------
+
+__device__ __forceinline__ void philox4x32_10(uint32_t (&c)[4], uint32_t k0, uint32_t k1) {
+#pragma unroll
+    for (int round = 0; round < 10; ++round) {
+        const uint64_t p0 = static_cast<uint64_t>(0xD2511F53u) * c[0];
+        const uint64_t p1 = static_cast<uint64_t>(0xCD9E8D57u) * c[2];
+        const uint32_t hi0 = static_cast<uint32_t>(p0 >> 32), lo0 = static_cast<uint32_t>(p0);
+        const uint32_t hi1 = static_cast<uint32_t>(p1 >> 32), lo1 = static_cast<uint32_t>(p1);
+        c[0] = hi1 ^ c[1] ^ k0;
+        c[1] = lo1;
+        c[2] = hi0 ^ c[3] ^ k1;
+        c[3] = lo0;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+}
+
+__global__ void __launch_bounds__(256) gaussian_kernel(const rch_gauss_job* __restrict__ jobs) {
+    const rch_gauss_job& J = jobs[blockIdx.y];
+    const int64_t total = J.rows * J.cols;
+    const int64_t group = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // elements 4 group .. + 3
+    if (4 * group >= total) return;
+    uint32_t c[4] = {static_cast<uint32_t>(group), static_cast<uint32_t>(group >> 32), 0u, 0u};
+    philox4x32_10(c, static_cast<uint32_t>(J.seed), static_cast<uint32_t>(static_cast<uint64_t>(J.seed) >> 32));
+    float z[4];
+#pragma unroll
+    for (int pair = 0; pair < 2; ++pair) {
+        // Uniforms in (0, 1]: (word + 1) * 2^-32 keeps log away from zero.
+        const float u1 = (static_cast<float>(c[2 * pair]) + 1.0f) * 2.3283064365386963e-10f;
+        const float u2 = static_cast<float>(c[2 * pair + 1]) * 2.3283064365386963e-10f;
+        const float r = sqrtf(-2.0f * logf(u1));
+        z[2 * pair] = r * cosf(6.283185307179586f * u2);
+        z[2 * pair + 1] = r * sinf(6.283185307179586f * u2);
+    }
+    RCH_GLOBAL float* dst = gout<float>(J.dst_ptr);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int64_t e = 4 * group + i;
+        if (e < total) {
+            const int64_t r = e / J.cols, col = e - r * J.cols;
+            dst[r * J.stride + col] = z[i];
+        }
+    }
+}
+
 int check_matrices(const rch_fit_matrix* mats, int n, int channels, const char* what) {
     if (!mats || n <= 0 || n > 65535) return fail(RCH_E_CONFIG, "%s: 1 <= n_mats <= 65535 required", what);
     if (channels <= 0 || channels % 8 != 0 || channels > (1 << 20))
@@ -748,6 +878,14 @@ int rch_cholesky_inverse(const double* a_dev, double* x_dev, int32_t* info_dev, 
     hipLaunchKernelGGL(cholesky_inverse_kernel, dim3(static_cast<unsigned>(n)), dim3(kCholThreads), 0, as_stream(stream),
                        a_dev, x_dev, info_dev, k);
     return check_launch("rch_cholesky_inverse");
+}
+
+int rch_fit_gaussian(const rch_gauss_job* jobs_dev, int n_jobs, int64_t max_elements, void* stream) {
+    if (!jobs_dev || n_jobs <= 0 || n_jobs > 65535 || max_elements <= 0 || (max_elements + 1023) / 1024 > 0x7fffffff)
+        return fail(RCH_E_CONFIG, "rch_fit_gaussian: invalid arguments");
+    const dim3 grid(static_cast<unsigned>((max_elements + 1023) / 1024), static_cast<unsigned>(n_jobs));
+    hipLaunchKernelGGL(gaussian_kernel, grid, dim3(256), 0, as_stream(stream), jobs_dev);
+    return check_launch("rch_fit_gaussian");
 }
 
 int rch_quantize_batched(const rch_quantize_job* jobs_dev, int n_jobs, int64_t max_rows, void* stream) {

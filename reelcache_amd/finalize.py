@@ -173,7 +173,8 @@ def _rank_terms(coefficients, rows):
     Gram -- fp16 products are exact in fp32 -- and its largest diagonal entry): a handful of
     batched launches for the whole group."""
     q = torch.stack(rows)
-    p = torch.stack([c.double() for c in coefficients]) if len({c.shape[0] for c in coefficients}) == 1 else None
+    # Tiles of one token count: one stack and one widening for the group.
+    p = torch.stack(coefficients).double() if len({c.shape[0] for c in coefficients}) == 1 else None
     if p is not None:
         products = torch.bmm(p.mT, p)
     else:  # tiles of different token counts: one product each

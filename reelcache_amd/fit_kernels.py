@@ -281,6 +281,26 @@ def cholesky_inverse(gram: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     return inverse, info
 
 
+def gaussian(blocks) -> None:
+    """Fill each ``(view, seed)`` of ``blocks`` with seeded standard normals in one launch: ``view``
+    an fp32 ``[rows, cols]`` device tensor with unit column stride (e.g. the trailing columns of a
+    start block), ``seed`` a 64-bit integer; the values depend only on the seed and the shape."""
+    blocks = list(blocks)
+    if not blocks:
+        return
+    device = _device([view for view, _ in blocks])
+    table = np.zeros(len(blocks), dtype=_lib.GAUSS_DTYPE)
+    for row, (view, seed) in zip(table, blocks):
+        if view.dtype != torch.float32 or view.ndim != 2 or view.stride(1) != 1 or min(view.shape) < 1:
+            raise ConfigurationError("Gaussian blocks are nonempty fp32 [rows, cols] views with unit column stride")
+        row["dst_ptr"], row["rows"], row["cols"], row["stride"] = view.data_ptr(), view.shape[0], view.shape[1], \
+            view.stride(0)
+        row["seed"] = np.int64(np.uint64(int(seed) % 2 ** 64).astype(np.int64))
+    descriptors = _upload(table, device)
+    _lib.call("rch_fit_gaussian", descriptors.data_ptr(), len(blocks), int((table["rows"] * table["cols"]).max()),
+              _stream(device))
+
+
 def column_extrema(values: torch.Tensor) -> torch.Tensor:
     """int32 [2 * cols] order keys of every column of an fp32 matrix: ~key(min) then key(max)
     (the layout :func:`split_keys` reads with ``rank = cols``)."""

@@ -43,6 +43,11 @@ def canonical_dtype(value: Any) -> str:
 def canonical_digest(value: Any) -> str:
     """SHA-256 hex digest of the canonical JSON of ``value`` (sorted keys, no whitespace, no NaN)."""
     def plain(item):
+        kind = type(item)
+        if kind is str or kind is int or kind is float or kind is bool or item is None:
+            return item  # the common leaves, without the abstract-class checks below
+        if kind is dict:
+            return {str(key): plain(child) for key, child in item.items()}
         if isinstance(item, Mapping):
             return {str(key): plain(child) for key, child in item.items()}
         if isinstance(item, (list, tuple)):

@@ -128,6 +128,37 @@ def test_energies_match_fp64(device, dtype):
     assert source_only[0, 0] == pytest.approx(of.energies(host)[1], rel=1e-12)
 
 
+def test_energies_on_both_rank_paths(device):
+    """Ranks up to 64 keep the coefficient block in registers, larger ones stream it: a ragged batch
+    over both paths (and a rank that is not a multiple of 4) matches the FP64 oracle, and so does the
+    fp32 residual matrix X - P Q (rounded once from its FP64 value)."""
+    rng = np.random.default_rng(21)
+    ranks = [13, 48, 64, 65, 130]
+    sources, hosts, bases, host_bases = [], [], [], []
+    for index, rank in enumerate(ranks):
+        x, host = _source(rng, 200 + 37 * index, 192, "bfloat16", device, spectrum=True)
+        q, q_host = _basis(rng, rank, 192, device)
+        sources.append(x)
+        hosts.append(host)
+        bases.append(q)
+        host_bases.append(q_host)
+    keys = fk.absmax(sources)
+    coefficients, _ = fk.project(sources, bases, ranks)
+    totals, residuals = fk.energies(sources, keys, bases=bases, ranks=ranks, coefficients=coefficients,
+                                    residuals=True)
+    totals = totals.cpu().numpy()
+    for total, residual, host, basis, p, rank in zip(totals, residuals, hosts, host_bases, coefficients, ranks):
+        p_host = p.cpu().numpy()
+        _, source, error = of.energies(host, basis, p_host, rank)
+        assert total[0] == pytest.approx(source, rel=1e-12), rank
+        assert total[1] == pytest.approx(error, rel=1e-12), rank
+        exact = of.as_float(host) - p_host.astype(np.float64) @ np.asarray(basis, np.float16).astype(np.float64)[:rank]
+        got = residual.cpu().numpy()
+        # FP64 sums in another order: the fp32 rounding agrees except next to a rounding boundary.
+        assert (got == exact.astype(np.float32)).mean() >= 0.999, rank
+        assert np.abs(got - exact).max() <= 2 ** -23 * np.abs(exact).max(), rank
+
+
 def test_zero_matrix_energies(device):
     x = torch.zeros((70, 64), dtype=torch.bfloat16, device=device)
     keys = fk.absmax([x])

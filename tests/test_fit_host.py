@@ -272,6 +272,40 @@ def test_bucket_prefixes_and_crossing():
         assert directions.crossing(fraction) == of.crossing(energies, energies.sum() * 1.01, fraction)
 
 
+def test_crossing_edges_and_shared_fp16_rows():
+    """Crossings at the exact boundary and past the last direction; FP16 rows from the batch's shared
+    conversion equal a per-set conversion, for every prefix and position."""
+    energies = torch.tensor([4.0, 2.0, 1.0, 1.0], dtype=torch.float64)
+    directions = rm.DirectionSet(torch.zeros(4, 3), energies, 10.0, False, "x")
+    assert [directions.crossing(f) for f in (0.4, 0.41, 0.6, 0.8, 0.81, 1.0)] == [1, 2, 2, 4, None, None]
+    assert rm.DirectionSet(torch.zeros(0, 3), energies[:0], 0.0, True, "x").crossing(0.5) == 0
+    batch = torch.randn(3, 5, 7, generator=torch.Generator().manual_seed(3)) * 100
+    half = rm._HalfRows(batch)
+    for position in range(3):
+        shared = rm.DirectionSet(batch[position], energies, 10.0, False, "x", half=(half, position))
+        alone = rm.DirectionSet(batch[position], energies, 10.0, False, "x")
+        for count in (1, 3, 5):
+            assert torch.equal(shared.rows16(count), alone.rows16(count))
+            assert shared.rows16(count).is_contiguous() and shared.rows16(count).dtype == torch.float16
+    assert sorted(half.prefixes) == [1, 3, 5]
+
+
+def test_batch_view_only_for_consecutive_slices():
+    base = torch.arange(5 * 4 * 3, dtype=torch.float32).reshape(5, 4, 3)
+    view = rm._batch_view([base[1], base[2], base[3]])
+    assert view is not None and torch.equal(view, base[1:4]) and view.data_ptr() == base[1].data_ptr()
+    sliced = rm._batch_view([base[0][:2], base[1][:2]])  # sub-blocks keep their strides
+    assert sliced is not None and torch.equal(sliced, base[:2, :2])
+    spaced = rm._batch_view([base[0], base[2], base[4]])  # evenly spaced blocks: a strided view
+    assert spaced is not None and torch.equal(spaced, base[0::2])
+    for tensors in ([base[0], base[1], base[3]], [base[2], base[1]], [base[1], base[2].clone()],
+                    [base[1][:2], base[2]], [base[1], base[2].double()]):
+        assert rm._batch_view(tensors) is None
+    grams = [base[0], base[2], base[1]]
+    assert torch.equal(rm._stack_grams(grams, [0, 2]), base[:2])
+    assert torch.equal(rm._stack_grams(grams, [1, 2]), torch.stack([base[2], base[1]]))
+
+
 def test_mosaic_matches_the_oracle_packer():
     rng = np.random.default_rng(5)
     for shape, fmt in (((3, 6, 8, 40), "yuv444p"), ((2, 4, 4, 100), "yuv420p"), ((1, 5, 3, 7), "yuv444p")):
