@@ -441,8 +441,9 @@ def longcat_leg(device, layers, reps):
     """Per-layer restore time at the LongCat shape: 16 chunks x 4680 tokens of K and V, 32 heads x
     128 in the [1, H, T, D] bf16 cache layout, per-chunk ranks U{256..512} on the 32-grid of one
     512-row orthonormal bf16 basis per layer and target, no RoPE (LongCat stores pre-RoPE K).
-    Timed with HIP events on the launch stream (pack -> last restore), alone and while a
-    4096 x 4096 bf16 GEMM runs on a second stream (the next chunk's forward)."""
+    Timed with HIP events on the launch stream (pack -> last restore), alone and while 4096 x 4096
+    bf16 GEMMs (the next chunk's forward) run on a second stream for the whole restore; the
+    GEMMs' own slowdown is reported beside the restore's."""
     from reelcache_amd import restore_kernels as rk
 
     rng = np.random.default_rng(5)
@@ -472,18 +473,36 @@ def longcat_leg(device, layers, reps):
     side = torch.cuda.Stream(device)
     a = torch.randn(4096, 4096, device=device, dtype=torch.bfloat16, generator=generator)
     b = torch.randn(4096, 4096, device=device, dtype=torch.bfloat16, generator=generator)
-    with torch.cuda.stream(side):
-        for _ in range(2):
-            a @ b
 
-    def timed(precision, mode):
-        times, variants = [], []
+    def products(count):
+        """``count`` back-to-back 4096^2 bf16 products on the side stream; (begin, end) events."""
+        begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(side):
+            begin.record(side)
+            for _ in range(count):
+                a @ b
+            end.record(side)
+        return begin, end
+
+    products(3)
+    torch.cuda.synchronize(device)
+    gemm_runs = []
+    for _ in range(3):
+        begin, end = products(10)
+        end.synchronize()
+        gemm_runs.append(begin.elapsed_time(end) / 10 * 1e3)
+    gemm_us = float(np.median(gemm_runs))  # one product alone
+
+    def timed(precision, count):
+        """Median restore time per layer (pack -> last launch) with ``count`` side products started
+        just before it (0: alone), and the side products' mean time per product."""
+        times, side_us, variants = [], [], []
         for _ in range(reps):
             for jobs in work:
-                if mode == "with_gemm":
+                window = None
+                if count:
                     side.wait_stream(stream)
-                    with torch.cuda.stream(side):
-                        a @ b
+                    window = products(count)
                 stage = []
                 handle = rk.reconstruct(jobs, stream=stream, stage_events=stage, precision=precision)
                 handle.release()
@@ -492,19 +511,30 @@ def longcat_leg(device, layers, reps):
                 side.synchronize()
                 events = dict(stage)
                 times.append(events["pack"].elapsed_time(events["fused"]) * 1e3)
-        return float(np.median(times)), variants
+                if window is not None:
+                    side_us.append(window[0].elapsed_time(window[1]) * 1e3 / count)
+        return float(np.median(times)), (float(np.median(side_us)) if side_us else None), variants
 
     results = {}
     for precision in ("fp16x2", "fp16"):
         for jobs in work:
             rk.reconstruct(jobs, stream=stream, precision=precision).release()
         torch.cuda.synchronize(device)
-        alone, variants = timed(precision, "alone")
-        with_gemm, _ = timed(precision, "with_gemm")
+        alone, _, variants = timed(precision, 0)
+        # Enough side products to cover the whole restore of a layer (and then some), so every
+        # restore launch runs beside a GEMM.
+        count = max(2, math.ceil(alone / gemm_us) + 1)
+        with_gemm, gemm_beside, _ = timed(precision, count)
         achieved = flops / (alone / 1e6) / 1e12
         passes = 2 if precision == "fp16x2" else 1
         results[precision] = {
             "kernel_us_per_layer": round(alone, 1), "kernel_us_per_layer_with_gemm": round(with_gemm, 1),
+            "side_gemm": {"products": count, "us_per_product_alone": round(gemm_us, 1),
+                          "us_per_product_beside_restore": round(gemm_beside, 1),
+                          "gemm_slowdown": round(gemm_beside / gemm_us, 3),
+                          "restore_slowdown": round(with_gemm / alone, 3),
+                          "what": "bf16 4096^2 products on a second stream, started just before the layer's "
+                                  "restore and covering all of it; slowdowns relative to each running alone"},
             "variants": variants,
             "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": 2500.0, "unit": "TFLOP/s",
                          "frac": round(achieved / 2500.0, 4), "mfma_work_tflops": round(passes * achieved, 1)}}
@@ -602,6 +632,38 @@ def fp16_leg(layers, device, steps):
 CAUSVID_LAYER_MS = (2.58, 0.486)
 
 
+def vendor_gemm_leg(device, reps=20):
+    """The library GEMM (torch.mm -> hipBLASLt) on the shape of each restore launch, as a yardstick
+    for the fused kernel: bf16 coefficients [7 x 4680, r] times a bf16 basis [r, 1536] into bf16,
+    with nothing else (no dequantization, RoPE or scatter), at the launch's rank r and at 2r (the
+    fused fp16x2 product's MFMA work).  Median of ``reps`` launches timed with events."""
+    rows = CHUNKS * TOKENS
+    generator = torch.Generator(device=device).manual_seed(11)
+    out = {}
+    for name, rank in (("K", RANK_K), ("V", RANK_V)):
+        entry = {}
+        for label, inner in (("rank", rank), ("equal_mfma_work", 2 * rank)):
+            a = torch.randn(rows, inner, device=device, dtype=torch.bfloat16, generator=generator)
+            b = torch.randn(inner, CHANNELS, device=device, dtype=torch.bfloat16, generator=generator)
+            for _ in range(3):
+                torch.mm(a, b)
+            times = []
+            for _ in range(reps):
+                begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                begin.record()
+                torch.mm(a, b)
+                end.record()
+                end.synchronize()
+                times.append(begin.elapsed_time(end) * 1e3)
+            entry[label] = {"k": inner, "us": round(float(np.median(times)), 2)}
+            del a, b
+        out[name] = entry
+    torch.cuda.synchronize(device)
+    return {"what": "torch.mm (hipBLASLt) bf16 [32760, k] x [k, 1536] -> bf16, k = the launch's rank and twice it "
+                    "(the fp16x2 product's MFMA work); compare restore_launch_us (which also dequantizes, "
+                    "rotates and scatters)", **out}
+
+
 def overlap_leg(layers, device, gemm=4096):
     """The CausVid step as a layer-overlapped restore (``overlapped_restore``): a producer thread
     restores the layers in order on a private stream while a consumer stream runs a stand-in
@@ -652,14 +714,46 @@ def overlap_leg(layers, device, gemm=4096):
     restore_ms = (time.perf_counter() - begin) * 1e3
     torch.cuda.synchronize(device)
     begin = time.perf_counter()
-    readiness = start_overlapped_restore(layers, device=device)
-    forward(readiness)
+    # Device clock of the overlapped run: `origin` on the consumer stream before anything starts
+    # (the restore is ordered after it), then per layer the consumer's need (it reached the layer)
+    # and its start (the layer's readiness wait passed); the readiness dates each layer's release.
+    origin = torch.cuda.Event(enable_timing=True)
+    origin.record(consumer)
+    readiness = start_overlapped_restore(layers, device=device, wait_event=origin)
+    marks = []
+    with torch.cuda.stream(consumer):
+        for layer in range(len(layers)):
+            needed, started = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            needed.record(consumer)
+            readiness.layer(layer).wait(consumer)
+            started.record(consumer)
+            for _ in range(reps):
+                a @ b
+            marks.append((needed, started))
+        finished = torch.cuda.Event(enable_timing=True)
+        finished.record(consumer)
     consumer.synchronize()
     overlapped_ms = (time.perf_counter() - begin) * 1e3
     readiness.join(timeout=120)
+    readiness.quiesce(timeout=120)
     waits = readiness.timeline()["waited_seconds"]
+    ready = readiness.device_ready_ms(origin)
     torch.cuda.synchronize(device)
+    per_layer = []
+    for layer, ((needed, started), ready_ms) in enumerate(zip(marks, ready)):
+        deadline = layer * layer_ms  # the consumer reaches layer L after L layers of compute c(h)
+        per_layer.append({"layer": layer, "ready_ms": round(ready_ms, 3), "deadline_ms": round(deadline, 3),
+                          "slack_ms": round(deadline - ready_ms, 3),
+                          "needed_ms": round(origin.elapsed_time(needed), 3),
+                          "stall_ms": round(needed.elapsed_time(started), 3)})
+    device_ms = origin.elapsed_time(finished)
     return {"layers": len(layers), "history_chunks": CHUNKS, "deadline_ms_per_layer": round(layer_ms, 3),
+            "per_layer": per_layer,
+            "layers_ready_by_deadline": sum(entry["slack_ms"] >= 0 for entry in per_layer),
+            "min_slack_ms": min(entry["slack_ms"] for entry in per_layer),
+            "consumer_stall_ms": round(sum(entry["stall_ms"] for entry in per_layer), 3),
+            "overlapped_device_ms": round(device_ms, 3),
+            "contention_ms": round(device_ms - forward_ms, 3),
             "forward_stand_in": f"{reps} bf16 [{gemm} x {gemm}] products per layer (c(h) = 2.58 + 0.486 h ms, "
                                 "reelcache/decoded_tier.py:49-50)",
             "forward_ms": round(forward_ms, 3), "restore_eager_ms": round(restore_ms, 3),
@@ -667,7 +761,11 @@ def overlap_leg(layers, device, gemm=4096):
             "exposed_restore_ms": round(overlapped_ms - forward_ms, 3),
             "consumer_host_wait_ms": round(sum(waits) * 1e3, 3),
             "what": "wall times; the overlapped run restores layer L on a private stream while the "
-                    "consumer's layer L waits for it (LayerReadiness)"}
+                    "consumer's layer L waits for it (LayerReadiness).  per_layer (device clock from the "
+                    "run's start): ready_ms = the layer's restore writes ended, deadline_ms = L x c(h) "
+                    "(when a forward running at c(h) per layer reaches it), needed_ms = when this "
+                    "consumer reached it, stall_ms = its wait there; contention_ms = overlapped device "
+                    "time - forward alone (the forward slowed by sharing the GPU plus any stalls)"}
 
 
 def main():
@@ -677,12 +775,14 @@ def main():
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--cpu-seconds", type=float, default=20.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--fit-steps", type=int, default=2, help="timed fit chunks (0 skips the fit leg)")
-    parser.add_argument("--fit-warmup", type=int, default=1)
+    parser.add_argument("--fit-steps", type=int, default=8, help="timed fit chunks (0 skips the fit leg)")
+    parser.add_argument("--fit-warmup", type=int, default=2)
     parser.add_argument("--longcat-layers", type=int, default=2,
                         help="LongCat-shape layers timed beside the headline (0 skips the leg)")
     parser.add_argument("--no-overlap-leg", dest="overlap_leg", action="store_false",
                         help="skip the layer-overlapped restore beside a stand-in forward")
+    parser.add_argument("--no-vendor-gemm-leg", dest="vendor_gemm_leg", action="store_false",
+                        help="skip timing the library GEMM on the restore launches' shapes")
     parser.add_argument("--no-fp16-leg", dest="fp16_leg", action="store_false",
                         help="skip the step timed in the single-product fp16 precision mode")
     parser.add_argument("--pictures-layers", type=int, default=4,
@@ -816,6 +916,10 @@ def main():
                           "host planning + enqueue overlapped with the device"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": dominant.get("traffic"),
+                     # The same ratio over the committed rocprofv3 kernel-trace duration of this launch.
+                     "rocprof_us": dominant.get("rocprof_us"),
+                     "frac_rocprof": round(dominant["algorithmic_bytes"] / dominant["rocprof_us"] / 1e3 / HBM_PEAK_GBS, 4)
+                     if dominant.get("rocprof_us") else None,
                      "kernel": "restore_fast_kernel<4, 12, false, 2, 2, 1>: the V launch of a layer call (7 jobs, "
                                "rank 192), the longest of the call's launches",
                      "algorithmic_bytes_per_launch": dominant["algorithmic_bytes"],
@@ -840,6 +944,8 @@ def main():
         result["fp16"] = fp16_leg(layers, device, args.steps)
     if args.overlap_leg:
         result["overlap"] = overlap_leg(layers, device)
+    if args.vendor_gemm_leg:
+        result["vendor_gemm"] = vendor_gemm_leg(device)
     if args.copy_probe:
         source = torch.empty(COPY_PROBE_BYTES, dtype=torch.uint8, device=device).fill_(7)
         target = torch.empty_like(source)

@@ -74,7 +74,8 @@ class LayerReadiness:
         self._error: BaseException | None = None
         self._unmarked = [(1 << len(names)) - 1] * layers
         gpu = self.device.type == "cuda"
-        self._events = [[torch.cuda.Event() if gpu else None for _ in names] for _ in range(layers)]
+        # Timing events: the consumer orders after them, and they date each layer's release.
+        self._events = [[torch.cuda.Event(enable_timing=True) if gpu else None for _ in names] for _ in range(layers)]
         self._threads: dict[str, threading.Thread] = {}
         self._finished: dict[str, float] = {}
         self.streams: dict[str, Any] = {}
@@ -227,6 +228,20 @@ class LayerReadiness:
                          first_layer_ready_seconds_from_call=min(marks) if marks else None,
                          last_layer_ready_seconds_from_call=max(marks) if marks else None,
                          restore_complete_seconds_from_call=max(self._finished.values()) - self.called_at)
+
+    def device_ready_ms(self, since: Any) -> list[float | None]:
+        """Per layer, device milliseconds from the timing event ``since`` (recorded by the caller
+        before the restore started) to the end of the layer's writes on every source's stream: the
+        latest source event.  None for a layer not released on a GPU stream.  Call after the
+        restore finished (e.g. after :meth:`quiesce`)."""
+        ready: list[float | None] = []
+        for layer in range(self.layers):
+            marked = [event for event in self._events[layer] if event is not None]
+            if self.marked_at[layer] is None or len(marked) != len(self.sources):
+                ready.append(None)
+                continue
+            ready.append(max(since.elapsed_time(event) for event in marked))
+        return ready
 
     def timeline(self) -> dict[str, Any]:
         """Marks (seconds after creation) and the consumer's host waits, per layer."""
