@@ -113,26 +113,40 @@ __global__ void __launch_bounds__(kThreads) absmax_kernel(const rch_fit_matrix* 
 }
 
 // ---------------------------------------------------------------------------------------------
-// Gram G = X^T X.  Workgroup = one 128 x 128 tile (ti >= tj) of one matrix; 4 waves, each a
-// 64 x 64 quadrant as 2 x 2 MFMA 32x32 blocks.  Rows are staged 32 per step into LDS as
-// [channel][row]: each lane loads a channel pair of 8 rows (coalesced along the row) and
-// writes the two channels' 8-row runs, so that an MFMA operand (8 consecutive rows of one
-// channel for 16-bit sources, 16 for fp32) is one or four 16-byte LDS reads.
-// Register-prefetched, double-buffered LDS, one barrier per step.
+// Gram G = X^T X.  Workgroup = one 256 x 256 tile (ti >= tj) of one matrix, 16 waves: wave w
+// computes the 64 x 64 quadrant (w / 4, w % 4) as 2 x 2 MFMA 32x32 blocks (on a diagonal tile
+// the quadrants above the diagonal are mirrors and are skipped), and stages a quarter of the
+// step's rows for 128 channels of one panel.  Rows are staged 32 per step into LDS as
+// [channel][row]: each lane loads a channel pair of 8 rows, coalesced along the row, and writes
+// the two channels' row runs, so that an MFMA operand (8 consecutive rows of one channel for
+// 16-bit sources, 16 for fp32) is one or four 16-byte LDS reads.  Register-prefetched two steps
+// ahead, double-buffered LDS, one barrier per step.
+//
+// The 21 tiles of a 1536-channel matrix run on one XCD (xcd_unit) and sweep the rows together,
+// so each row band of X is fetched from HBM about once and then read from that XCD's L2 by the
+// six tiles of each panel.  Every output element sums its products in row order, 16 rows (2 for
+// fp32) per MFMA, so the result does not depend on the tile size or the rows per step.
 // ---------------------------------------------------------------------------------------------
 
-constexpr int kGramTile = 128;
-constexpr int kGramRows = 32;
+constexpr int kGramTile = 256;
+constexpr int kGramThreads = 1024;
+
+// Rows staged per step (a wave stages a quarter of them).  Measured on MI355X, 32-row steps with
+// loads two steps ahead beat 64-row steps (which leave registers for one step ahead only).
+template <int DT>
+constexpr int gram_rows() {
+    return 32;
+}
 
 template <int DT>
 constexpr int gram_pitch() {
-    return DT == RCH_DT_F32 ? kGramRows * 4 + 16 : kGramRows * 2 + 16;  // bytes per staged channel
+    return gram_rows<DT>() * esize<DT>() + 16;  // bytes per staged channel
 }
 
 template <int DT>
 struct GramStage {
     typedef typename std::conditional<DT == RCH_DT_F32, u2, uint32_t>::type word;
-    word d[8];  // rows r0 .. r0 + 7 of this lane's channel pair
+    word d[gram_rows<DT>() / 4];  // rows r0 .. of this lane's channel pair
 };
 
 template <int DT>
@@ -142,7 +156,7 @@ __device__ __forceinline__ void gram_load(GramStage<DT>& st, const rch_fit_matri
     const uint32_t offset = c < channels ? static_cast<uint32_t>(c * E) : kOutOfRange;
     const uint32_t row_bytes = static_cast<uint32_t>(M->src_stride * E);
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
+    for (int r = 0; r < gram_rows<DT>() / 4; ++r) {
         if constexpr (DT == RCH_DT_F32)
             st.d[r] = __builtin_amdgcn_raw_buffer_load_b64(src, offset + r * row_bytes, 0, 0);
         else
@@ -150,29 +164,38 @@ __device__ __forceinline__ void gram_load(GramStage<DT>& st, const rch_fit_matri
     }
 }
 
+// The stage's two channels, each as a run of rows/4 consecutive rows at row offset
+// group * rows / 4 of the channel's staged row block.
 template <int DT>
-__device__ __forceinline__ void gram_store(const GramStage<DT>& st, unsigned char* tile, int lane, int wave) {
+__device__ __forceinline__ void gram_store(const GramStage<DT>& st, unsigned char* tile, int lane, int group) {
     constexpr int P = gram_pitch<DT>();
     unsigned char* c0 = tile + (2 * lane) * P;
     unsigned char* c1 = c0 + P;
     if constexpr (DT == RCH_DT_F32) {
+        static_assert(gram_rows<DT>() == 32, "fp32 stages hold 8 rows per lane");
         const u4 a0 = {st.d[0][0], st.d[1][0], st.d[2][0], st.d[3][0]};
         const u4 a1 = {st.d[4][0], st.d[5][0], st.d[6][0], st.d[7][0]};
         const u4 b0 = {st.d[0][1], st.d[1][1], st.d[2][1], st.d[3][1]};
         const u4 b1 = {st.d[4][1], st.d[5][1], st.d[6][1], st.d[7][1]};
-        *reinterpret_cast<u4*>(c0 + 32 * wave) = a0;
-        *reinterpret_cast<u4*>(c0 + 32 * wave + 16) = a1;
-        *reinterpret_cast<u4*>(c1 + 32 * wave) = b0;
-        *reinterpret_cast<u4*>(c1 + 32 * wave + 16) = b1;
+        *reinterpret_cast<u4*>(c0 + 32 * group) = a0;
+        *reinterpret_cast<u4*>(c0 + 32 * group + 16) = a1;
+        *reinterpret_cast<u4*>(c1 + 32 * group) = b0;
+        *reinterpret_cast<u4*>(c1 + 32 * group + 16) = b1;
     } else {
-        u4 lo, hi;
+        constexpr int kRuns = gram_rows<DT>() / 32;  // 8-row runs (16 bytes) per lane and channel
+        static_assert(kRuns >= 1 && 8 * kRuns == sizeof(st.d) / sizeof(st.d[0]), "stage rows");
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            lo[q] = (st.d[2 * q] & 0xffffu) | (st.d[2 * q + 1] << 16);
-            hi[q] = (st.d[2 * q] >> 16) | (st.d[2 * q + 1] & 0xffff0000u);
+        for (int run = 0; run < kRuns; ++run) {  // rows 8 run .. 8 run + 7 of the stage
+            u4 lo, hi;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t even = st.d[8 * run + 2 * q], odd = st.d[8 * run + 2 * q + 1];
+                lo[q] = (even & 0xffffu) | (odd << 16);
+                hi[q] = (even >> 16) | (odd & 0xffff0000u);
+            }
+            *reinterpret_cast<u4*>(c0 + 16 * kRuns * group + 16 * run) = lo;
+            *reinterpret_cast<u4*>(c1 + 16 * kRuns * group + 16 * run) = hi;
         }
-        *reinterpret_cast<u4*>(c0 + 16 * wave) = lo;
-        *reinterpret_cast<u4*>(c1 + 16 * wave) = hi;
     }
 }
 
@@ -202,9 +225,9 @@ __device__ __forceinline__ void gram_mfma(f16v (&acc)[2][2], const unsigned char
                     acc[x][y] =
                         __builtin_amdgcn_mfma_f32_32x32x2f32(a[x][s >> 2][s & 3], b[y][s >> 2][s & 3], acc[x][y], 0, 0, 0);
     } else {
-        // Two 16-row steps; lane half h holds rows 16 ks + 8h .. + 7.
+        // 16-row MFMA steps; lane half h holds rows 16 ks + 8h .. + 7.
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
+        for (int ks = 0; ks < gram_rows<DT>() / 16; ++ks) {
             u4 a[2], b[2];
 #pragma unroll
             for (int x = 0; x < 2; ++x) {
@@ -227,8 +250,8 @@ __device__ __forceinline__ void gram_mfma(f16v (&acc)[2][2], const unsigned char
 }
 
 template <int DT>
-__global__ void __launch_bounds__(kThreads) gram_kernel(const rch_fit_matrix* __restrict__ mats, int channels, int tiles,
-                                                        int grid) {
+__global__ void __launch_bounds__(kGramThreads) gram_kernel(const rch_fit_matrix* __restrict__ mats, int channels,
+                                                            int tiles, int grid) {
     constexpr int P = gram_pitch<DT>();
     __shared__ __attribute__((aligned(16))) unsigned char lds[2][2][kGramTile * P];
 
@@ -243,9 +266,17 @@ __global__ void __launch_bounds__(kThreads) gram_kernel(const rch_fit_matrix* __
     const bool diagonal = ti == tj;
     const rch_fit_matrix* M = mats + mat;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int ci = ti * kGramTile + 2 * lane, cj = tj * kGramTile + 2 * lane;
-    const int steps = static_cast<int>((M->rows + kGramRows - 1) / kGramRows);
+    // Staging role: panel (0: the ti columns, 1: the tj columns), 128-channel half, 8-row group.
+    const int panel = wave >> 3, half = (wave >> 2) & 1, group = wave & 3;
+    // A diagonal tile stages one panel: the other panel's waves load from an out-of-range column
+    // (the buffer loads return zeros without a memory access), so every wave runs the same
+    // straight-line loop and the loads stay in flight across the MFMAs.
+    const int c = diagonal && panel == 1 ? channels : (panel ? tj : ti) * kGramTile + 128 * half + 2 * lane;
+    // MFMA role: the 64 x 64 quadrant (wm, wn).
+    const int wm = wave >> 2, wn = wave & 3;
+    const bool computes = !(diagonal && wm < wn);
+    constexpr int kRows = gram_rows<DT>();
+    const int steps = static_cast<int>((M->rows + kRows - 1) / kRows);
 
     f16v acc[2][2];
 #pragma unroll
@@ -253,32 +284,51 @@ __global__ void __launch_bounds__(kThreads) gram_kernel(const rch_fit_matrix* __
 #pragma unroll
         for (int y = 0; y < 2; ++y) acc[x][y] = f16v{};
 
-    GramStage<DT> si, sj;
-    gram_load<DT>(si, M, channels, 8 * wave, ci);
-    if (!diagonal) gram_load<DT>(sj, M, channels, 8 * wave, cj);
-    gram_store<DT>(si, lds[0][0], lane, wave);
-    if (!diagonal) gram_store<DT>(sj, lds[0][1], lane, wave);
-    __syncthreads();
-    for (int step = 0; step < steps; ++step) {
+    // 16-bit rows are loaded two steps ahead into alternating register stages: the loads for
+    // step s + 2 are issued before step s's MFMAs and written to LDS after step s + 1's, so two
+    // steps of MFMA work cover their latency.  Rows past the end read as zeros (empty buffer), so
+    // the loads and stores need no conditions and the loop stays straight-line, which keeps the
+    // compiler's waits on the older stage only.
+    unsigned char* staged = lds[0][panel] + 128 * half * P;  // this wave's rows in buffer 0
+    constexpr int kBuffer = 2 * kGramTile * P;                // buffer 1 = buffer 0 + kBuffer
+    auto mfma_step = [&](int step) {
         const int buf = step & 1;
-        const bool more = step + 1 < steps;
-        if (more) {
-            const int64_t r0 = static_cast<int64_t>(step + 1) * kGramRows + 8 * wave;
-            gram_load<DT>(si, M, channels, r0, ci);
-            if (!diagonal) gram_load<DT>(sj, M, channels, r0, cj);
-        }
-        gram_mfma<DT>(acc, lds[buf][0], diagonal ? lds[buf][0] : lds[buf][1], wm, wn, lane);
-        if (more) {
-            gram_store<DT>(si, lds[buf ^ 1][0], lane, wave);
-            if (!diagonal) gram_store<DT>(sj, lds[buf ^ 1][1], lane, wave);
-        }
+        if (computes) gram_mfma<DT>(acc, lds[buf][0], diagonal ? lds[buf][0] : lds[buf][1], wm, wn, lane);
+        return staged + (buf ^ 1) * kBuffer;  // where the next step's rows go
+    };
+    if constexpr (DT != RCH_DT_F32) {
+        GramStage<DT> sa, sb;
+        gram_load<DT>(sa, M, channels, kRows / 4 * group, c);
+        gram_load<DT>(sb, M, channels, kRows + kRows / 4 * group, c);
+        gram_store<DT>(sa, staged, lane, group);
         __syncthreads();
+        auto step_body = [&](int step, GramStage<DT>& ahead, const GramStage<DT>& next) {
+            gram_load<DT>(ahead, M, channels, static_cast<int64_t>(step + 2) * kRows + kRows / 4 * group, c);
+            gram_store<DT>(next, mfma_step(step), lane, group);
+            __syncthreads();
+        };
+        for (int step = 0; step < steps; step += 2) {
+            step_body(step, sa, sb);
+            if (step + 1 < steps) step_body(step + 1, sb, sa);
+        }
+    } else {  // fp32 stages are twice as large: one step ahead keeps the loop within 128 VGPRs
+        GramStage<DT> st;
+        gram_load<DT>(st, M, channels, kRows / 4 * group, c);
+        gram_store<DT>(st, staged, lane, group);
+        __syncthreads();
+        for (int step = 0; step < steps; ++step) {
+            gram_load<DT>(st, M, channels, static_cast<int64_t>(step + 1) * kRows + kRows / 4 * group, c);
+            gram_store<DT>(st, mfma_step(step), lane, group);
+            __syncthreads();
+        }
     }
+    if (!computes) return;
 
     // Accumulator element e of lane l: row 8 (e / 4) + 4 (l / 32) + e % 4, column l % 32.
     RCH_GLOBAL float* G = gout<float>(M->gram_ptr);
     const int64_t ld = M->gram_stride;
     const int h = lane >> 5, col = lane & 31;
+    const bool lower_only = diagonal && wm == wn;  // a quadrant on the diagonal: its lower half, mirrored
 #pragma unroll
     for (int x = 0; x < 2; ++x)
 #pragma unroll
@@ -290,7 +340,7 @@ __global__ void __launch_bounds__(kThreads) gram_kernel(const rch_fit_matrix* __
             for (int g = 0; g < 4; ++g) {
                 const int64_t i0 = ib + 8 * g + 4 * h;  // rows i0 .. i0 + 3 (channels % 8 == 0: all or none in range)
                 if (i0 >= channels) continue;
-                if (!diagonal) {
+                if (!lower_only) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) G[(i0 + r) * ld + j] = acc[x][y][4 * g + r];
                     // Mirror: G[j][i0 .. i0 + 3] is one 16-byte store.
@@ -795,13 +845,15 @@ int check_matrices(const rch_fit_matrix* mats, int n, int channels, const char* 
 
 using namespace rch;
 
-#define RCH_DISPATCH_DTYPE(dtype, what, KERNEL, GRID, ...)                                                          \
+#define RCH_DISPATCH_DTYPE_BLOCK(dtype, what, KERNEL, GRID, BLOCK, ...)                                             \
     switch (dtype) {                                                                                                \
-        case RCH_DT_BF16: hipLaunchKernelGGL(KERNEL<RCH_DT_BF16>, GRID, dim3(kThreads), 0, s, __VA_ARGS__); break; \
-        case RCH_DT_F16: hipLaunchKernelGGL(KERNEL<RCH_DT_F16>, GRID, dim3(kThreads), 0, s, __VA_ARGS__); break;   \
-        case RCH_DT_F32: hipLaunchKernelGGL(KERNEL<RCH_DT_F32>, GRID, dim3(kThreads), 0, s, __VA_ARGS__); break;   \
+        case RCH_DT_BF16: hipLaunchKernelGGL(KERNEL<RCH_DT_BF16>, GRID, dim3(BLOCK), 0, s, __VA_ARGS__); break;     \
+        case RCH_DT_F16: hipLaunchKernelGGL(KERNEL<RCH_DT_F16>, GRID, dim3(BLOCK), 0, s, __VA_ARGS__); break;       \
+        case RCH_DT_F32: hipLaunchKernelGGL(KERNEL<RCH_DT_F32>, GRID, dim3(BLOCK), 0, s, __VA_ARGS__); break;       \
         default: return fail(RCH_E_CONFIG, "%s: source dtype must be bf16, f16 or f32", what);                      \
     }
+#define RCH_DISPATCH_DTYPE(dtype, what, KERNEL, GRID, ...) \
+    RCH_DISPATCH_DTYPE_BLOCK(dtype, what, KERNEL, GRID, kThreads, __VA_ARGS__)
 
 extern "C" {
 
@@ -824,8 +876,8 @@ int rch_fit_gram(const rch_fit_matrix* mats_dev, int n_mats, int channels, int s
     if (tiles * n_mats > 0x7fffffff) return fail(RCH_E_CONFIG, "rch_fit_gram: too many tiles");
     const int grid = static_cast<int>(tiles * n_mats);
     hipStream_t s = as_stream(stream);
-    RCH_DISPATCH_DTYPE(src_dtype, "rch_fit_gram", gram_kernel, dim3(grid), mats_dev, channels, static_cast<int>(tiles),
-                       grid);
+    RCH_DISPATCH_DTYPE_BLOCK(src_dtype, "rch_fit_gram", gram_kernel, dim3(grid), kGramThreads, mats_dev, channels,
+                             static_cast<int>(tiles), grid);
     return check_launch("rch_fit_gram");
 }
 

@@ -56,7 +56,8 @@ def test_absmax_exact_and_nonfinite(device, dtype):
 
 
 @pytest.mark.parametrize("dtype,rows,channels", [("bfloat16", 300, 136), ("float16", 257, 256),
-                                                 ("float32", 129, 200), ("bfloat16", 4680, 1536)])
+                                                 ("float32", 129, 200), ("bfloat16", 4680, 1536),
+                                                 ("float16", 97, 520), ("float32", 70, 392), ("bfloat16", 33, 768)])
 def test_gram_symmetric_and_within_fp32_bound(device, dtype, rows, channels):
     rng = np.random.default_rng(11)
     sources, hosts = zip(*[_source(rng, rows - 7 * i, channels, dtype, device) for i in range(2)])
