@@ -887,14 +887,22 @@ def main():
     value = LAYERS * written / (ms_per_step / 1e3) / 1e9
     kernel_avg = float(np.mean(kernel_ms))
     # Live per-launch durations (HIP events on the launch stream around each launch of the
-    # stage-event step): K, then V; the pack before them.
-    k_us, v_us = (float(v) * 1e3 for v in np.mean(np.array(launch_ms), axis=0)[:2])
+    # stage-event step), the pack before them: one pair launch per layer call (K and V groups
+    # together, the default), or K then V when the groups launch one by one.
+    launch_us = [float(v) * 1e3 for v in np.mean(np.array(launch_ms), axis=0)]
     pack_us = float(np.mean(pack_ms)) * 1e3
     profile = profile_figures()
     pack_bytes = 2 * (RANK_K + RANK_V) * CHANNELS * 2
+    if len(launch_us) == 1:
+        launches = (("KV", launch_bytes(RANK_K) + launch_bytes(RANK_V), launch_us[0]),)
+        kernel = ("restore_pair_kernel<4, 2, 8, 12>: the K (7 jobs, rank 128, RoPE) and V (7 jobs, rank 192) launch "
+                  "groups of a layer call in one launch")
+    else:
+        launches = (("K", launch_bytes(RANK_K), launch_us[0]), ("V", launch_bytes(RANK_V), launch_us[1]))
+        kernel = ("restore_fast_kernel<4, 12, false, 2, 2, 1>: the V launch of a layer call (7 jobs, rank 192), the "
+                  "longest of the call's launches")
     split = {}
-    for name, rank, us in (("K", RANK_K, k_us), ("V", RANK_V, v_us), ("pack", None, pack_us)):
-        nbytes = launch_bytes(rank) if rank else pack_bytes
+    for name, nbytes, us in launches + (("pack", pack_bytes, pack_us),):
         entry = {"us": round(us, 2), "algorithmic_bytes": nbytes, "achieved_gbs": round(nbytes / us / 1e3, 1),
                  "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
         if f"traffic_bytes_per_launch {name}" in profile:
@@ -903,8 +911,8 @@ def main():
         if f"mfma_busy {name}" in profile:
             entry["mfma_busy"] = profile[f"mfma_busy {name}"]
         split[name] = entry
-    dominant = split["V"]
-    launches_avg = (k_us + v_us) / 1e3
+    dominant = split[launches[-1][0]]
+    launches_avg = sum(launch_us) / 1e3
     achieved = dominant["achieved_gbs"]
     result = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -931,8 +939,7 @@ def main():
                      "rocprof_us": dominant.get("rocprof_us"),
                      "frac_rocprof": round(dominant["algorithmic_bytes"] / dominant["rocprof_us"] / 1e3 / HBM_PEAK_GBS, 4)
                      if dominant.get("rocprof_us") else None,
-                     "kernel": "restore_fast_kernel<4, 12, false, 2, 2, 1>: the V launch of a layer call (7 jobs, "
-                               "rank 192), the longest of the call's launches",
+                     "kernel": kernel,
                      "algorithmic_bytes_per_launch": dominant["algorithmic_bytes"],
                      "launch_us": dominant["us"],
                      "traffic_source": "profiles/restore_causvid_counters.md (rocprofv3 FETCH_SIZE + WRITE_SIZE per "

@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-#define RCH_ABI_VERSION 10
+#define RCH_ABI_VERSION 11
 
 /* Status codes (mapped to reelcache errors by the host). */
 #define RCH_OK 0
@@ -213,6 +213,29 @@ int rch_restore(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev, i
  */
 int rch_restore_occupancy(int precision, int source_kind, int max_ksteps, int head_dim, int out_dtype, int group_flags,
                           int* blocks_per_cu);
+
+/*
+ * Two launch groups of one call in one launch: a RoPE group and a plain group,
+ * both RCH_GF_FAST | RCH_GF_HEAD_PAIRS with the same channels, head_dim,
+ * source kinds (uint8 rows or pictures) and output dtype (f16 or bf16), each of
+ * at most 12 rank steps, in fp16x2.  tiles_dev holds the RoPE group's
+ * n_tiles0 tiles, then the plain group's n_tiles1; bounds_dev [grid + 1] splits
+ * the concatenated head-pair units (as rch_restore with RCH_GF_HEAD_PAIRS) into
+ * cost-balanced ranges.  Same values as one rch_restore per group; the grid
+ * fills and drains once.  Replaces the per-group launches of _fused_group
+ * (reelcache/restore_kernels.py:2025-2062) for a call's K and V groups.
+ */
+int rch_restore_pair(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev, int n_tiles0, int n_tiles1,
+                     const int32_t* bounds_dev, int grid, int channels, int head_dim, int source_kind, int out_dtype,
+                     int precision, int ksteps0, int ksteps1, const int32_t* scratch_dev, void* stream);
+
+/*
+ * Resident workgroups per CU of the rch_restore_pair kernel for these
+ * arguments; 0 (and RCH_OK) when no pair kernel is compiled for them, in which
+ * case the groups launch one by one.
+ */
+int rch_restore_pair_occupancy(int precision, int source_kind, int ksteps0, int ksteps1, int head_dim, int out_dtype,
+                               int* blocks_per_cu);
 
 /*
  * One entry of a channel-slice restore launch: 32-token tiles [tile0 + u0, tile0 + u1) of one

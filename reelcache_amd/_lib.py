@@ -16,7 +16,7 @@ import numpy as np
 from .errors import ConfigurationError, UnsupportedError
 
 LIBRARY = Path(__file__).resolve().with_name("libreelcache_hip.so")
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 # Status codes (RCH_E_*).
 OK, E_CONFIG, E_UNSUPPORTED, E_LAUNCH = 0, 1, 2, 3
@@ -76,6 +76,8 @@ _SIGNATURES = {
     "rch_coefficient_bound": ([_p, _i, _p, _i, _i, _p, _p], _i),
     "rch_restore": ([_p, _i, _p, _i, _p, _i, _i, _i, _i, _i, _i, _i, _i, _p, _p], _i),
     "rch_restore_occupancy": ([_i, _i, _i, _i, _i, _i, ctypes.POINTER(_i)], _i),
+    "rch_restore_pair": ([_p, _i, _p, _i, _i, _p, _i, _i, _i, _i, _i, _i, _i, _i, _p, _p], _i),
+    "rch_restore_pair_occupancy": ([_i, _i, _i, _i, _i, _i, ctypes.POINTER(_i)], _i),
     "rch_slice_entry_size": ([], _i),
     "rch_restore_slice_blocks": ([_i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i)], _i),
     "rch_restore_sliced": ([_p, _i, _p, _i, _p, _i, _p, _i, _i, _i, _i, _i, _i, _i, _p, _p], _i),
@@ -185,6 +187,16 @@ def occupancy(precision: int, source_kind: int, max_ksteps: int, head_dim: int, 
     """Resident workgroups per CU of the restore variant for these arguments."""
     blocks = ctypes.c_int(0)
     call("rch_restore_occupancy", precision, source_kind, max_ksteps, head_dim, out_dtype, group_flags,
+         ctypes.byref(blocks))
+    return blocks.value
+
+
+def pair_occupancy(precision: int, source_kind: int, ksteps0: int, ksteps1: int, head_dim: int,
+                   out_dtype: int) -> int:
+    """Resident workgroups per CU of the pair kernel for two head-pair groups (a RoPE group of
+    ``ksteps0`` rank steps, then a plain one of ``ksteps1``); 0 when none is compiled for them."""
+    blocks = ctypes.c_int(0)
+    call("rch_restore_pair_occupancy", precision, source_kind, ksteps0, ksteps1, head_dim, out_dtype,
          ctypes.byref(blocks))
     return blocks.value
 

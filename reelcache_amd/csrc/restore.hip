@@ -641,6 +641,57 @@ int rch_restore(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev, i
     return check_launch("rch_restore");
 }
 
+// The pair kernel of two head-pair groups, or nullptr when none is compiled for them.
+static PairFn pick_pair_launch(int precision, int source_kind, int ksteps0, int ksteps1, int head_dim, int out_dtype,
+                               int* chosen0, int* chosen1) {
+    *chosen0 = *chosen1 = 0;
+    if (head_dim % 32 || ksteps0 <= 0 || ksteps1 <= 0 ||
+        (source_kind != RCH_SRC_U8 && source_kind != RCH_SRC_PICTURE))
+        return nullptr;
+    // fp16x2 only: in the single-product modes the two groups' units cost about the same and one
+    // launch per group measured as fast.
+    return precision == RCH_PREC_FP16X2 ? pick_pair_fp16x2(ksteps0, ksteps1, out_dtype, chosen0, chosen1) : nullptr;
+}
+
+int rch_restore_pair_occupancy(int precision, int source_kind, int ksteps0, int ksteps1, int head_dim, int out_dtype,
+                               int* blocks_per_cu) {
+    if (!blocks_per_cu) return fail(RCH_E_CONFIG, "rch_restore_pair_occupancy: invalid arguments");
+    *blocks_per_cu = 0;
+    int chosen0 = 0, chosen1 = 0;
+    const PairFn fn = pick_pair_launch(precision, source_kind, ksteps0, ksteps1, head_dim, out_dtype, &chosen0,
+                                       &chosen1);
+    if (!fn) return RCH_OK;  // no pair kernel: the groups launch one by one
+    int blocks = 0;
+    const hipError_t error = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, kThreads, 0);
+    if (error != hipSuccess)
+        return fail(RCH_E_LAUNCH, "rch_restore_pair_occupancy: %s", hipGetErrorString(error));
+    *blocks_per_cu = blocks;
+    return RCH_OK;
+}
+
+int rch_restore_pair(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev, int n_tiles0, int n_tiles1,
+                     const int32_t* bounds_dev, int grid, int channels, int head_dim, int source_kind, int out_dtype,
+                     int precision, int ksteps0, int ksteps1, const int32_t* scratch_dev, void* stream) {
+    if (!scratch_dev || n_tiles0 <= 0 || n_tiles1 <= 0 || n_tiles0 > 0x7fffffff - n_tiles1)
+        return fail(RCH_E_CONFIG, "rch_restore_pair: invalid launch arguments");
+    const int flags = RCH_GF_FAST | RCH_GF_HEAD_PAIRS;
+    int status = check_restore_args("rch_restore_pair", jobs_dev, n_jobs, tiles_dev, n_tiles0 + n_tiles1, bounds_dev,
+                                    grid, channels, head_dim, out_dtype, ksteps0 > ksteps1 ? ksteps0 : ksteps1, flags);
+    if (status) return status;
+    int chosen0 = 0, chosen1 = 0;
+    const PairFn fn = pick_pair_launch(precision, source_kind, ksteps0, ksteps1, head_dim, out_dtype, &chosen0,
+                                       &chosen1);
+    if (!fn)
+        return fail(RCH_E_CONFIG, "rch_restore_pair: no pair kernel covers precision %d, output dtype %d, %d and %d "
+                    "rank steps", precision, out_dtype, ksteps0, ksteps1);
+    // Units of the first group: its tiles x head-pair units per tile (checked above to fit int32).
+    const int heads = channels / head_dim;
+    const int split_unit = n_tiles0 * ((heads / 2) * (head_dim / 32));
+    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, as_stream(stream), jobs_dev,
+                       tiles_dev, bounds_dev, scratch_dev, int64_t(0), heads, head_dim, split_unit);
+    return check_launch("rch_restore_pair");
+}
+
 // The channel-slice kernel (restore_slice.h) for a group, or nullptr when none is compiled for
 // its rank / output / precision.
 static SliceFn pick_slice_launch(int precision, int max_ksteps, int out_dtype, int group_flags, int* max_blocks) {

@@ -35,6 +35,30 @@ struct Cursor {
 template <int KS, bool ROPE, int HP>
 constexpr int kFastOccupancy = HP == 2 ? 2 : (((KS <= 12 && !ROPE) || (KS <= 8 && ROPE)) ? 3 : 2);
 
+// LDS and fragment geometry of one straight-line variant.
+template <int PREC, int KS, int HP, int SPLIT>
+struct FastGeometry {
+    static constexpr int kThreadsT = kThreads * SPLIT;  // threads of the workgroup
+    static constexpr int kStepFrags = 64;               // u4 fragments of one 16-rank step of one block
+    static constexpr int kHeadFrags = KS * kStepFrags;  // fragments of one block (one head)
+    static constexpr int kBuffer = HP * kHeadFrags;     // u4 fragments of one step's LDS buffer
+    static constexpr int kRanks = KS * 16;
+    static constexpr int kPitch = kRanks + 8;
+    // Rank halves: the high half's partial sums of a step, [step parity][token group][16][64 lanes]
+    // fp32, share the codes buffer (codes are read only between the barriers of a tile entry).
+    static constexpr int kReduceBytes = SPLIT == 2 ? 2 * 4 * 16 * 64 * 4 : 0;
+    static constexpr int kCodesBytes = kTileTokens * kPitch > kReduceBytes ? kTileTokens * kPitch : kReduceBytes;
+};
+
+// LDS of a straight-line launch: two step buffers of basis fragments, the staged codes (or the
+// rank halves' partial sums), the staged affine and the picture cell offsets.
+struct FastLds {
+    u4* lds;
+    uint8_t* codes;
+    float* affine;
+    int64_t* cell_offset;
+};
+
 // HP = heads per step: 1, or 2 (RCH_GF_HEAD_PAIRS, an even head count): a step then computes the
 // same 32-channel dim block of two adjacent heads, so the per-step bookkeeping, barrier and
 // waits are shared by twice the matrix work and each RoPE pair set serves both heads.
@@ -44,37 +68,34 @@ constexpr int kFastOccupancy = HP == 2 ? 2 : (((KS <= 12 && !ROPE) || (KS <= 8 &
 // product, and the high half hands its fp32 partial sums to the low half through LDS, which
 // adds them and runs the epilogue (the only difference from one chain: the fp32 summation
 // order of the two halves).
+//
+// One workgroup's part of a launch: work units [first_unit, first_unit + steps) of the tile
+// table (unit u: tile u / (blocks per tile), then dim block and head).
 template <int PREC, int KS, bool ROPE, int OUT, int HP, int SPLIT>
-__global__ void __launch_bounds__(kThreads * SPLIT, (SPLIT == 2 ? 1 : kFastOccupancy<KS, ROPE, HP>))
-restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict__ tiles,
-                    const int32_t* __restrict__ bounds, const int32_t* __restrict__ scratch, int64_t pack_base,
-                    int heads, int head_dim) {
+__device__ __forceinline__ void fast_range(const rch_job* __restrict__ jobs, const int32_t* __restrict__ tiles,
+                                           const int first_unit, const int steps,
+                                           const int32_t* __restrict__ scratch, int64_t pack_base, int heads,
+                                           int head_dim, const FastLds& shared) {
     static_assert(PREC != RCH_PREC_FP32, "the fp32 mode runs restore_kernel");
     static_assert(HP == 1 || HP == 2, "one or two heads per step");
     static_assert(SPLIT == 1 || (SPLIT == 2 && HP == 1 && KS % 8 == 0), "rank halves: one head per step");
-    constexpr int kThreadsT = kThreads * SPLIT;          // threads of the workgroup
+    using G = FastGeometry<PREC, KS, HP, SPLIT>;
+    constexpr int kThreadsT = G::kThreadsT;
     constexpr int kKsWave = KS / SPLIT;                  // rank steps held by one wave
-    constexpr int kStepFrags = 64;                       // u4 fragments of one 16-rank step of one block
-    constexpr int kHeadFrags = KS * kStepFrags;          // fragments of one block (one head)
-    constexpr int kBuffer = HP * kHeadFrags;
+    constexpr int kStepFrags = G::kStepFrags;
+    constexpr int kHeadFrags = G::kHeadFrags;
+    constexpr int kBuffer = G::kBuffer;
     constexpr int kPer = kBuffer / kThreadsT;
     static_assert(kBuffer % kThreadsT == 0, "KS must be a multiple of 4: every thread moves whole fragments");
-    constexpr int kRanks = KS * 16;
-    constexpr int kPitch = kRanks + 8;
+    constexpr int kRanks = G::kRanks;
+    constexpr int kPitch = G::kPitch;
     constexpr bool kFp16 = PREC == RCH_PREC_FP16 || PREC == RCH_PREC_FP16X2;
     constexpr int kEsize = OUT == RCH_DT_F32 ? 4 : 2;
-    // Rank halves: the high half's partial sums of a step, [step parity][token group][16][64 lanes]
-    // fp32, share the codes buffer (codes are read only between the barriers of a tile entry).
-    constexpr int kReduceBytes = SPLIT == 2 ? 2 * 4 * 16 * 64 * 4 : 0;
-    constexpr int kCodesBytes = kTileTokens * kPitch > kReduceBytes ? kTileTokens * kPitch : kReduceBytes;
-    __shared__ u4 lds[2][kBuffer];
-    __shared__ __attribute__((aligned(16))) uint8_t codes[kCodesBytes];
-    __shared__ __attribute__((aligned(16))) float affine[2 * kRanks];
-    __shared__ int64_t cell_offset[kRanks];    // pictures: byte offset of rank column k's cell in a picture
+    u4* const lds = shared.lds;
+    uint8_t* const codes = shared.codes;
+    float* const affine = shared.affine;
+    int64_t* const cell_offset = shared.cell_offset;
 
-    const int range = xcd_unit(blockIdx.x, gridDim.x);
-    const int first_unit = bounds[range];
-    const int steps = bounds[range + 1] - first_unit;
     if (steps <= 0) return;
     const int head_blocks = head_dim >> 5;
     const int head_steps = heads / HP;  // steps per dim block
@@ -130,7 +151,7 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
     };
     auto commit = [&](int buffer, const u4 (&from)[kPer]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) lds[buffer][tid + i * kThreadsT] = from[i];
+        for (int i = 0; i < kPer; ++i) lds[buffer * kBuffer + tid + i * kThreadsT] = from[i];
     };
 
     // Per-lane state of the current tile.
@@ -409,7 +430,7 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
         // Basis fragments are read from LDS three steps ahead of their products (a rotating
         // window of four registers per head).
         constexpr int kAhead = kKsWave < 3 ? kKsWave : 3;
-        const u4* frags = &lds[buffer][lane] + half * kKsWave * kStepFrags;
+        const u4* frags = lds + buffer * kBuffer + lane + half * kKsWave * kStepFrags;
         u4 window[HP][kAhead + 1];
 #pragma unroll
         for (int j = 0; j < kAhead; ++j) {
@@ -536,9 +557,59 @@ restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict_
     }
 }
 
+// One launch group: workgroup b runs units [bounds[b'], bounds[b' + 1]) (b' = XCD-swizzled index).
+template <int PREC, int KS, bool ROPE, int OUT, int HP, int SPLIT>
+__global__ void __launch_bounds__(kThreads * SPLIT, (SPLIT == 2 ? 1 : kFastOccupancy<KS, ROPE, HP>))
+restore_fast_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict__ tiles,
+                    const int32_t* __restrict__ bounds, const int32_t* __restrict__ scratch, int64_t pack_base,
+                    int heads, int head_dim) {
+    using G = FastGeometry<PREC, KS, HP, SPLIT>;
+    __shared__ u4 lds[2 * G::kBuffer];
+    __shared__ __attribute__((aligned(16))) uint8_t codes[G::kCodesBytes];
+    __shared__ __attribute__((aligned(16))) float affine[2 * G::kRanks];
+    __shared__ int64_t cell_offset[G::kRanks];  // pictures: byte offset of rank column k's cell in a picture
+    const int range = xcd_unit(blockIdx.x, gridDim.x);
+    const int first_unit = bounds[range];
+    fast_range<PREC, KS, ROPE, OUT, HP, SPLIT>(jobs, tiles, first_unit, bounds[range + 1] - first_unit, scratch,
+                                               pack_base, heads, head_dim, FastLds{lds, codes, affine, cell_offset});
+}
+
+// Two head-pair launch groups of one call in one persistent launch: the tile table holds the
+// first group's tiles (RoPE, KS0 rank steps) and then the second's (no RoPE, KS1 steps); units
+// below split_unit (the first group's tiles x blocks per tile) run the first variant, the others
+// the second, and one cost-balanced split of the concatenated units covers both.  One grid ramps
+// up and drains once per call instead of once per group; each unit's arithmetic is the single
+// group kernel's, so the output bits are the same.
+template <int PREC, int OUT, int KS0, int KS1>
+__global__ void __launch_bounds__(kThreads, 2)
+restore_pair_kernel(const rch_job* __restrict__ jobs, const int32_t* __restrict__ tiles,
+                    const int32_t* __restrict__ bounds, const int32_t* __restrict__ scratch, int64_t pack_base,
+                    int heads, int head_dim, int split_unit) {
+    using G0 = FastGeometry<PREC, KS0, 2, 1>;
+    using G1 = FastGeometry<PREC, KS1, 2, 1>;
+    constexpr int kBuffer = G0::kBuffer > G1::kBuffer ? G0::kBuffer : G1::kBuffer;
+    constexpr int kCodes = G0::kCodesBytes > G1::kCodesBytes ? G0::kCodesBytes : G1::kCodesBytes;
+    constexpr int kRanks = G0::kRanks > G1::kRanks ? G0::kRanks : G1::kRanks;
+    __shared__ u4 lds[2 * kBuffer];
+    __shared__ __attribute__((aligned(16))) uint8_t codes[kCodes];
+    __shared__ __attribute__((aligned(16))) float affine[2 * kRanks];
+    __shared__ int64_t cell_offset[kRanks];
+    const FastLds shared{lds, codes, affine, cell_offset};
+    const int range = xcd_unit(blockIdx.x, gridDim.x);
+    const int begin = bounds[range], end = bounds[range + 1];
+    // Every step of a range ends with a workgroup barrier, so the second variant may refill the
+    // LDS the first one used as soon as it starts.
+    const int end0 = min(end, split_unit), begin1 = max(begin, split_unit);
+    fast_range<PREC, KS0, true, OUT, 2, 1>(jobs, tiles, begin, end0 - begin, scratch, pack_base, heads, head_dim,
+                                            shared);
+    fast_range<PREC, KS1, false, OUT, 2, 1>(jobs, tiles, begin1, end - begin1, scratch, pack_base, heads, head_dim,
+                                             shared);
+}
+
 // Kernel arguments: jobs, tiles, bounds, scratch words, pack_base (added to every rch_job.pack_ptr:
 // 0 for absolute fragment addresses), heads, head_dim.
 typedef void (*FastFn)(const rch_job*, const int32_t*, const int32_t*, const int32_t*, int64_t, int, int);
+typedef void (*PairFn)(const rch_job*, const int32_t*, const int32_t*, const int32_t*, int64_t, int, int, int);
 
 // Work-unit shape of a straight-line launch.
 enum FastShape : int { kOneHead = 0, kHeadPairs = 1, kRankHalves = 2 };
@@ -592,6 +663,36 @@ FastFn pick_fast(int ks, bool rope, int out_dtype, int shape, int* chosen) {
     }
 }
 
+template <int PREC, int OUT, int KS0>
+PairFn pair_second(int ks1, int* chosen1) {
+    if (ks1 <= 4) { *chosen1 = 4; return restore_pair_kernel<PREC, OUT, KS0, 4>; }
+    if (ks1 <= 8) { *chosen1 = 8; return restore_pair_kernel<PREC, OUT, KS0, 8>; }
+    if (ks1 <= 12) { *chosen1 = 12; return restore_pair_kernel<PREC, OUT, KS0, 12>; }
+    *chosen1 = 0;
+    return nullptr;
+}
+
+template <int PREC, int OUT>
+PairFn pair_first(int ks0, int ks1, int* chosen0, int* chosen1) {
+    if (ks0 <= 4) { *chosen0 = 4; return pair_second<PREC, OUT, 4>(ks1, chosen1); }
+    if (ks0 <= 8) { *chosen0 = 8; return pair_second<PREC, OUT, 8>(ks1, chosen1); }
+    if (ks0 <= 12) { *chosen0 = 12; return pair_second<PREC, OUT, 12>(ks1, chosen1); }
+    *chosen0 = *chosen1 = 0;
+    return nullptr;
+}
+
+// The pair kernel of a (RoPE group, plain group) of head-pair units, or nullptr (bf16 and f16
+// outputs, up to 12 rank steps per group).
+template <int PREC>
+PairFn pick_pair(int ks0, int ks1, int out_dtype, int* chosen0, int* chosen1) {
+    *chosen0 = *chosen1 = 0;
+    switch (out_dtype) {
+        case RCH_DT_F16: return pair_first<PREC, RCH_DT_F16>(ks0, ks1, chosen0, chosen1);
+        case RCH_DT_BF16: return pair_first<PREC, RCH_DT_BF16>(ks0, ks1, chosen0, chosen1);
+        default: return nullptr;
+    }
+}
+
 }  // namespace
 
 // One per precision translation unit (restore_<precision>.hip); nullptr when no fast variant
@@ -599,5 +700,8 @@ FastFn pick_fast(int ks, bool rope, int out_dtype, int shape, int* chosen) {
 FastFn pick_fast_fp16(int ks, bool rope, int out_dtype, int shape, int* chosen);
 FastFn pick_fast_fp16x2(int ks, bool rope, int out_dtype, int shape, int* chosen);
 FastFn pick_fast_bf16(int ks, bool rope, int out_dtype, int shape, int* chosen);
+
+// Pair kernels (restore_pair_fp16x2.hip): fp16x2 products.
+PairFn pick_pair_fp16x2(int ks0, int ks1, int out_dtype, int* chosen0, int* chosen1);
 
 }  // namespace rch

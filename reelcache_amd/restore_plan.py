@@ -34,11 +34,19 @@ TILE_TOKENS = 128  # tokens per workgroup tile (4 waves x 32)
 SLICE_TOKENS = 32  # tokens per tile of the channel-slice kernel (one wave's MFMA columns)
 BASIS_DTYPES = (torch.float16, torch.bfloat16)
 _DEFAULT_CONFIG = {"TILE_TOKENS": TILE_TOKENS, "BLOCK_N": 32, "waves": 4, "workgroups_per_cu": None,
-                   "store_cost": 4.0, "fast_variant": True, "slice_variant": False, "head_pairs": True,
-                   "split_rank": True, "static_scratch": False, "stream_variant": False}
+                   "store_cost": None, "fast_variant": True, "slice_variant": False, "head_pairs": True,
+                   "split_rank": True, "static_scratch": False, "stream_variant": False,
+                   "pair_launch": True}
 DEFAULT_MERGED = dict(_DEFAULT_CONFIG)  # the merged configuration of calls without overrides (never modified)
 
 _DEVICE_INFO: dict = {}
+
+# A work unit's cost for the balanced split of a launch is store_cost + rank steps x MFMA passes.
+# The constant is the unit's work besides its products (tile entry share, epilogue, stores, fetch,
+# barrier) in units of one 16-rank product step, fitted on MI355X to the measured time of a
+# rank-128 RoPE unit against a rank-192 plain unit (CausVid K and V: 44 / 51 us per launch in
+# fp16x2, 42 / 42 us in fp16).  A pair launch mixes both, so the split must weigh them right.
+_STORE_COST = {"fp16x2": 48.0, "fp16": 120.0, "bf16": 120.0, "fp32": 4.0, "tf32": 4.0, "tf32x3": 4.0}
 
 
 def _compute_units(device):
@@ -613,7 +621,8 @@ class _Layout:
             groups.setdefault(key, []).append(index)
         compute_units = _compute_units(device)
         passes = 2 if precision == "fp16x2" else (4 if precision == "fp32" else 1)
-        store_cost = float(_config_value(config, "store_cost"))
+        store_cost = _config_value(config, "store_cost")
+        store_cost = float(_STORE_COST[precision] if store_cost is None else store_cost)
         plans = []
         for key, members in groups.items():
             kind, group_flags = key[0], key[-1]
@@ -665,18 +674,70 @@ class _Layout:
                     and (channels // head_dim) % 2 == 0 and max_ksteps <= _PAIRS_MAX_KSTEPS):
                 group_flags |= _lib.GF_HEAD_PAIRS  # a work unit: one dim block of two heads
             blocks_per_tile = (channels + 31) // 32 // (2 if group_flags & _lib.GF_HEAD_PAIRS else 1)
-            per_cu = config.get("workgroups_per_cu") or _occupancy(self.code, kind, max_ksteps, head_dim,
-                                                                   plan["out_dtype"], group_flags)
-            grid = int(max(1, min(len(tiles) * blocks_per_tile, compute_units * max(1, per_cu))))
             steps = np.array([job_steps[i] for i in tiles[:, 0].tolist()], dtype=np.float64)
-            bounds = _balanced_bounds(steps * passes + store_cost, blocks_per_tile, grid)
             plan.update(variant="general" if not group_flags & _lib.GF_FAST
                         else ("pairs" if group_flags & _lib.GF_HEAD_PAIRS
                               else ("split" if group_flags & _lib.GF_SPLIT_RANK else "fast")),
-                        tiles=arena.add(tiles), n_tiles=len(tiles), bounds=arena.add(bounds), grid=grid,
-                        flags=group_flags)
+                        flags=group_flags, tile_rows=tiles, tile_costs=steps * passes + store_cost,
+                        blocks_per_tile=blocks_per_tile)
+        if not self.static and bool(_config_value(config, "pair_launch")):
+            plans = self._pair_groups(plans)
+        for plan in plans:
+            tiles = plan.pop("tile_rows", None)
+            if tiles is None:
+                continue
+            costs, blocks_per_tile = plan.pop("tile_costs"), plan.pop("blocks_per_tile")
+            if plan["variant"] == "pair":
+                per_cu = config.get("workgroups_per_cu") or _lib.pair_occupancy(
+                    self.code, plan["kind"], plan["ksteps0"], plan["ksteps1"], plan["head_dim"], plan["out_dtype"])
+            else:
+                per_cu = config.get("workgroups_per_cu") or _occupancy(self.code, plan["kind"], plan["max_ksteps"],
+                                                                       plan["head_dim"], plan["out_dtype"],
+                                                                       plan["flags"])
+            grid = int(max(1, min(len(tiles) * blocks_per_tile, compute_units * max(1, per_cu))))
+            bounds = _balanced_bounds(costs, blocks_per_tile, grid)
+            plan.update(tiles=arena.add(tiles), n_tiles=len(tiles), bounds=arena.add(bounds), grid=grid)
             self.grids.append(grid)
             self.variants.append(plan["variant"])
+        return plans
+
+    def _pair_groups(self, plans):
+        """Merges a RoPE head-pair group with a plain head-pair group of the same geometry (a call's
+        K and V) into one ``pair`` launch when a pair kernel covers them (``rch_restore_pair``):
+        the concatenated units get one cost-balanced split, so the persistent grid fills and drains
+        once per call instead of once per group."""
+        candidates = [plan for plan in plans if plan.get("variant") == "pairs"]
+        for first in candidates:
+            if not first["flags"] & _lib.GF_ROPE or first.get("paired"):
+                continue
+            for second in candidates:
+                if second["flags"] & _lib.GF_ROPE or second.get("paired"):
+                    continue
+                if any(first[name] != second[name] for name in ("channels", "head_dim", "out_dtype")):
+                    continue
+                # The straight-line kernel reads uint8 rows or pictures per job, so either kind pairs.
+                kinds = {first["kind"], second["kind"]}
+                if not kinds <= {_lib.SRC_U8, _lib.SRC_PICTURE}:
+                    continue
+                kind = _lib.SRC_PICTURE if _lib.SRC_PICTURE in kinds else _lib.SRC_U8
+                if _lib.pair_occupancy(self.code, kind, first["max_ksteps"], second["max_ksteps"],
+                                       first["head_dim"], first["out_dtype"]) <= 0:
+                    continue
+                first["paired"] = second["paired"] = True
+                merged = {"kind": kind, "members": first["members"] + second["members"],
+                          "channels": first["channels"], "head_dim": first["head_dim"],
+                          "out_dtype": first["out_dtype"], "variant": "pair",
+                          "max_ksteps": max(first["max_ksteps"], second["max_ksteps"]),
+                          "ksteps0": first["max_ksteps"], "ksteps1": second["max_ksteps"],
+                          "flags": _lib.GF_FAST | _lib.GF_HEAD_PAIRS, "n_tiles0": len(first["tile_rows"]),
+                          "n_tiles1": len(second["tile_rows"]),
+                          "tile_rows": np.concatenate([first["tile_rows"], second["tile_rows"]]),
+                          "tile_costs": np.concatenate([first["tile_costs"], second["tile_costs"]]),
+                          "blocks_per_tile": first["blocks_per_tile"]}
+                plans = [merged if plan is first else plan for plan in plans if plan is not second]
+                break
+        for plan in plans:
+            plan.pop("paired", None)
         return plans
 
     def _staged_plan(self, descs, plan, basis_groups, arena):
@@ -885,6 +946,10 @@ class _Layout:
                 _lib.call("rch_restore_sliced", table, jobs, base + plan["tiles"], plan["n_tiles"], base + plan["entries"],
                           plan["n_entries"], base + plan["bounds"], plan["grid"], plan["channels"], plan["head_dim"],
                           plan["out_dtype"], self.code, plan["max_ksteps"], plan["flags"], scratch_base, hip_stream)
+            elif variant == "pair":
+                _lib.call("rch_restore_pair", table, jobs, base + plan["tiles"], plan["n_tiles0"], plan["n_tiles1"],
+                          base + plan["bounds"], plan["grid"], plan["channels"], plan["head_dim"], plan["kind"],
+                          plan["out_dtype"], self.code, plan["ksteps0"], plan["ksteps1"], scratch_base, hip_stream)
             elif self.static:
                 group = np.ascontiguousarray(packs[plan["packs"]])
                 _lib.call("rch_restore_noalloc", group.ctypes.data, len(group), table, jobs, base + plan["tiles"],

@@ -84,10 +84,10 @@ def test_fast_matches_general_and_oracle(device, precision, out_dtype):
 
 
 def test_fast_pictures_and_mixed_groups(device):
-    """Pictures and uint8 sources, K (RoPE) and V (none) jobs in one call: the call splits into
-    one straight-line launch per (source kind, RoPE) group (two heads per step: the head count
-    is even); with the channel-slice variant enabled, the uint8 rows take it and the pictures
-    stay on the straight-line kernel."""
+    """Pictures and uint8 sources, K (RoPE) and V (none) jobs in one call: the (source kind, RoPE)
+    groups (two heads per step: the head count is even) run as one pair launch, bit-identical to
+    one straight-line launch per group; with the channel-slice variant enabled, the uint8 rows
+    take it and the pictures stay on the straight-line kernel."""
     rng = np.random.default_rng(31)
     table = rk.RopeTable.from_complex(torch.from_numpy(orc.wan_freqs(64, 64)))
     heads, head_dim, grid, tokens = 4, 64, (2, 12, 14), 336
@@ -103,9 +103,15 @@ def test_fast_pictures_and_mixed_groups(device):
                                out_dtype="bfloat16", device=device))
     handle = rk.reconstruct([case.job for case in cases])
     handle.release()
-    assert sorted(handle.stats["variants"]) == ["pairs", "pairs"]
+    assert handle.stats["variants"] == ["pair"]  # the K (pictures, RoPE) and V groups in one launch
     for case in cases:
         _check_bound(case, "fp16x2")
+    paired = [case.job.destination.slot(case.job.tokens).clone() for case in cases]
+    handle = rk.reconstruct([case.job for case in cases], config={"pair_launch": False})
+    handle.release()
+    assert sorted(handle.stats["variants"]) == ["pairs", "pairs"]
+    for case, want in zip(cases, paired):
+        assert torch.equal(case.job.destination.slot(case.job.tokens), want)  # same bits, one launch per group
     handle = rk.reconstruct([case.job for case in cases], config={"slice_variant": True})
     handle.release()
     assert sorted(handle.stats["variants"]) == ["pairs", "sliced"]

@@ -178,7 +178,7 @@ def test_causvid_full_jobs_in_a_bf16_cache(device):
                                out_dtype="bfloat16", device=device))
     handle = rk.reconstruct([case.job for case in cases])
     handle.release()
-    assert set(handle.stats["variants"]) == {"pairs"}, handle.stats["variants"]
+    assert handle.stats["variants"] == ["pair"], handle.stats["variants"]
     for case in (cases[6], cases[11]):  # the K job of chunk 3, the V job of chunk 5
         values, bound = expected(case, "fp16x2")
         out = written(case)
@@ -197,3 +197,41 @@ def test_empty_call_and_errors(device):
         rk.reconstruct([case.job], precision="tf32")
     with pytest.raises(rk.UnsupportedError):
         rk.reconstruct([case.job], backend="staged")
+
+
+def test_causvid_pair_launch_equals_one_launch_per_group(device):
+    """The call's K and V groups in one pair launch write the same bits as one launch per group
+    (the default planner pairs them in fp16x2; ``pair_launch=False`` launches each group alone),
+    on the CausVid layer shape with mixed ranks per group and RoPE rows per chunk."""
+    precision = "fp16x2"
+    rng = np.random.default_rng(31)
+    heads, head_dim, grid = 12, 128, (3, 30, 52)
+    tokens = 4680
+    table = rk.RopeTable.from_complex(torch.from_numpy(orc.wan_freqs(head_dim, 64)))
+    bases = [torch.from_numpy(np.linalg.qr(rng.standard_normal((1536, rows)))[0].T.copy()).to(torch.bfloat16)
+             .to(device) for rows in (112, 192)]
+    caches = [destination("BTHD", 7 * tokens, heads, head_dim, "bfloat16", device) for _ in range(2)]
+    cases = []
+    for chunk in range(7):
+        cases.append(make_case(rng, grid=grid, heads=heads, head_dim=head_dim, rank=112 - 16 * (chunk % 2),
+                               view=rk.NativeView(caches[0], token_offset=chunk * tokens), basis=bases[0],
+                               table=table, rope_rows=(3 * chunk, 0, 0), out_dtype="bfloat16", device=device))
+        cases.append(make_case(rng, grid=grid, heads=heads, head_dim=head_dim, rank=192 - 16 * (chunk % 4),
+                               view=rk.NativeView(caches[1], token_offset=chunk * tokens), basis=bases[1],
+                               rope="none", out_dtype="bfloat16", device=device))
+    jobs = [case.job for case in cases]
+    handle = rk.reconstruct(jobs, precision=precision)
+    handle.release()
+    assert handle.stats["variants"] == ["pair"], handle.stats["variants"]
+    paired = [cache.clone() for cache in caches]
+    for cache in caches:
+        cache.zero_()
+    handle = rk.reconstruct(jobs, precision=precision, config={"pair_launch": False})
+    handle.release()
+    assert sorted(handle.stats["variants"]) == ["pairs", "pairs"]
+    for cache, want in zip(caches, paired):
+        assert torch.equal(cache, want)
+    for case in (cases[2], cases[9]):  # a K job (rank 112) and a V job (rank 160)
+        values, bound = expected(case, precision)
+        excess = np.abs(written(case) - values) - bound
+        assert float(excess.max()) <= 0, f"{int((excess > 0).sum())} of {excess.size} elements exceed the bound"
