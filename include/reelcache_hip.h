@@ -478,7 +478,7 @@ int rch_fit_gaussian(const rch_gauss_job* jobs_dev, int n_jobs, int64_t max_elem
  * definite k x k matrices A (row-major, contiguous, only the upper triangle read), R upper with
  * A = R^T R and x = R^{-1} (upper, zeros below).  info[b] = 0, or j + 1 when the leading minor of
  * order j + 1 is not positive definite (LAPACK's convention), x[b] is then the identity.
- * 1 <= k <= RCH_CHOLESKY_MAX_K (one workgroup per matrix, the matrix in LDS).
+ * 1 <= k <= RCH_CHOLESKY_MAX_K (one workgroup per matrix, its upper triangle in LDS).
  * Replaces the torch.linalg.cholesky_ex + trsm_right_upper pair of each CholeskyQR step
  * (reelcache/rank_method.py:738-752, :676-685).
  */

@@ -710,73 +710,103 @@ __global__ void __launch_bounds__(kThreads) quantize_batched_kernel(const rch_qu
 
 // ---------------------------------------------------------------------------------------------
 // Batched FP64 Cholesky factor and triangular inverse (the planner's CholeskyQR steps): one
-// workgroup per k x k matrix held row-major in LDS.  Right-looking factorization, one column per
-// step: the pivot row is scaled by 1 / sqrt(pivot) (one reciprocal, kept for the solve), then
-// the trailing upper triangle takes the rank-1 update.  The inverse X = R^-1 is solved row by row from the bottom (lane c owns column
-// c): row i of R is copied aside, then X[i][c] = -(sum_{p > i} R[i][p] X[p][c]) / R[i][i] overwrites
-// R[i][c] -- every lane reads the same R[i][p] and neighbouring X[p][c], so LDS reads do not
-// conflict, and rows below i of R are no longer needed.
+// 1024-thread workgroup per k x k matrix, whose upper triangle lives in LDS in packed row-major
+// form, with one workgroup barrier per factor column and one per inverse row.
+//
+// Factorization (right-looking): in step j every thread reads the pivot d = A[j][j], forms
+// 1 / sqrt(d) itself and applies the rank-1 update A[i][c] -= (A[j][i] / r)(A[j][c] / r) to its
+// share of the trailing triangle j < i <= c, reading row j unscaled (no thread writes row j in
+// step j).  The scaled row j = row j of R goes to a row buffer and is written back into the
+// triangle in step j + 1, when no thread reads row j.
+//
+// Inverse X = R^-1, rows from the bottom: S[r][c] accumulates sum_{p > r} R[r][p] X[p][c] as rows
+// p are finished.  In step i, row i is final: X[i][c] = (delta_ic - S[i][c]) / R[i][i]; every
+// thread forms the values of row i it needs from S[i][c] and adds R[r][i] X[i][c] into S[r][c]
+// for its share of r < i <= c.  Row i of X goes to a row buffer and replaces row i of S in step
+// i - 1.  Lanes run over columns and waves over rows, so a wave's LDS accesses are one row of
+// consecutive doubles plus one broadcast word.
 // ---------------------------------------------------------------------------------------------
 
-constexpr int kCholThreads = 512;
+constexpr int kCholThreads = 1024;
+constexpr int kCholWaves = kCholThreads / 64;
+constexpr int kCholPacked = RCH_CHOLESKY_MAX_K * (RCH_CHOLESKY_MAX_K + 1) / 2;
+
+// Offset of (i, c), i <= c, in a packed upper triangle of order k (rows i = 0.. stored back to back).
+__device__ __forceinline__ int packed_at(int i, int c, int k) { return i * k - (i * (i - 1)) / 2 + (c - i); }
 
 __global__ void __launch_bounds__(kCholThreads) cholesky_inverse_kernel(const double* __restrict__ a,
                                                                          double* __restrict__ x,
                                                                          int32_t* __restrict__ info, int k) {
-    __shared__ double m[RCH_CHOLESKY_MAX_K * RCH_CHOLESKY_MAX_K];
-    __shared__ double diag[RCH_CHOLESKY_MAX_K], row[RCH_CHOLESKY_MAX_K];
-    const int tid = threadIdx.x;
+    __shared__ double m[kCholPacked];   // A, then R (off-diagonal; the diagonal keeps the pivots)
+    __shared__ double s[kCholPacked];   // S, then X
+    __shared__ double rowbuf[2][RCH_CHOLESKY_MAX_K];
+    __shared__ double diag[RCH_CHOLESKY_MAX_K];  // 1 / R[j][j]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t base = static_cast<int64_t>(blockIdx.x) * k * k;
     const RCH_GLOBAL double* A = gin<double>(reinterpret_cast<int64_t>(a)) + base;
     RCH_GLOBAL double* X = gout<double>(reinterpret_cast<int64_t>(x)) + base;
-    for (int e = tid; e < k * k; e += kCholThreads) m[e] = A[e];
+    for (int i = wave; i < k; i += kCholWaves) {
+        for (int c = i + lane; c < k; c += 64) {
+            m[packed_at(i, c, k)] = A[i * k + c];
+            s[packed_at(i, c, k)] = 0.0;
+        }
+    }
     __syncthreads();
     int failed = 0;
     for (int j = 0; j < k; ++j) {
-        const double d = m[j * k + j];  // every thread reads the same pivot: the branch is uniform
+        const double d = m[packed_at(j, j, k)];  // every thread reads the same pivot: the branch is uniform
         if (!(d > 0.0) || !(d < INFINITY)) {
             failed = j + 1;
             break;
         }
-        const double r = sqrt(d), inv = 1.0 / r;
-        for (int c = j + 1 + tid; c < k; c += kCholThreads) m[j * k + c] *= inv;
-        __syncthreads();
-        if (tid == 0) diag[j] = inv;  // the reciprocal of R[j][j]
-        // Trailing upper triangle: lanes over columns (the pivot row's entry of the column in a
-        // register), waves over rows; the rows of a lane are independent updates.
-        for (int c = j + 1 + (tid & 63); c < k; c += 64) {
-            const double q = m[j * k + c];
-#pragma unroll 4
-            for (int i = j + 1 + (tid >> 6); i <= c; i += kCholThreads / 64) m[i * k + c] -= m[j * k + i] * q;
+        const double inv = 1.0 / sqrt(d);
+        if (j > 0) {  // row j - 1 of R, scaled in the previous step
+            for (int c = j + tid; c < k; c += kCholThreads) m[packed_at(j - 1, c, k)] = rowbuf[(j - 1) & 1][c];
+        }
+        const int row_j = packed_at(j, j, k) - j;  // row j's entry c sits at row_j + c
+        for (int c = j + 1 + tid; c < k; c += kCholThreads) rowbuf[j & 1][c] = m[row_j + c] * inv;
+        if (tid == 0) diag[j] = inv;
+        for (int i = j + 1 + wave; i < k; i += kCholWaves) {
+            const double ri = m[row_j + i] * inv;
+            const int row_i = packed_at(i, i, k) - i;
+            for (int c = i + lane; c < k; c += 64) {
+                const double rc = m[row_j + c] * inv;
+                const double product = ri * rc;
+                m[row_i + c] = m[row_i + c] - product;
+            }
         }
         __syncthreads();
     }
     if (failed) {
-        for (int i = tid >> 6; i < k; i += kCholThreads / 64)
-            for (int c = tid & 63; c < k; c += 64) X[i * k + c] = i == c ? 1.0 : 0.0;
+        for (int i = wave; i < k; i += kCholWaves)
+            for (int c = lane; c < k; c += 64) X[i * k + c] = i == c ? 1.0 : 0.0;
         if (tid == 0) info[blockIdx.x] = failed;
         return;
     }
+    // Step k - 1 wrote row k - 2 back and row k - 1 has no off-diagonal entry: m holds R above
+    // the diagonal (the last step's barrier makes it visible).
     for (int i = k - 1; i >= 0; --i) {
-        for (int c = i + 1 + tid; c < k; c += kCholThreads) row[c] = m[i * k + c];
-        __syncthreads();
-        for (int c = i + tid; c < k; c += kCholThreads) {
-            // Four partial sums keep four LDS reads in flight.
-            double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
-            int p = i + 1;
-            for (; p + 3 <= c; p += 4) {
-                s0 += row[p] * m[p * k + c];
-                s1 += row[p + 1] * m[(p + 1) * k + c];
-                s2 += row[p + 2] * m[(p + 2) * k + c];
-                s3 += row[p + 3] * m[(p + 3) * k + c];
+        const double di = diag[i];
+        const int srow_i = packed_at(i, i, k) - i;
+        if (i + 1 < k) {  // row i + 1 of X, finished in the previous step
+            for (int c = i + 1 + tid; c < k; c += kCholThreads) s[packed_at(i + 1, c, k)] = rowbuf[(i + 1) & 1][c];
+        }
+        for (int c = i + tid; c < k; c += kCholThreads) rowbuf[i & 1][c] = ((c == i ? 1.0 : 0.0) - s[srow_i + c]) * di;
+        for (int r = wave; r < i; r += kCholWaves) {
+            const double rri = m[packed_at(r, i, k)];
+            const int srow_r = packed_at(r, r, k) - r;
+            for (int c = i + lane; c < k; c += 64) {
+                const double xic = ((c == i ? 1.0 : 0.0) - s[srow_i + c]) * di;
+                const double product = rri * xic;
+                s[srow_r + c] = s[srow_r + c] + product;
             }
-            for (; p <= c; ++p) s0 += row[p] * m[p * k + c];
-            m[i * k + c] = ((c == i ? 1.0 : 0.0) - ((s0 + s1) + (s2 + s3))) * diag[i];
         }
         __syncthreads();
     }
-    for (int i = tid >> 6; i < k; i += kCholThreads / 64)
-        for (int c = tid & 63; c < k; c += 64) X[i * k + c] = i <= c ? m[i * k + c] : 0.0;
+    for (int c = tid; c < k; c += kCholThreads) s[packed_at(0, c, k)] = rowbuf[0][c];
+    __syncthreads();
+    for (int i = wave; i < k; i += kCholWaves)
+        for (int c = lane; c < k; c += 64) X[i * k + c] = i <= c ? s[packed_at(i, c, k)] : 0.0;
     if (tid == 0) info[blockIdx.x] = 0;
 }
 
