@@ -70,3 +70,40 @@ def test_captured_restore_replays_match_eager(device, config, ranks):
             assert torch.equal(cache, want), f"replay {replay} differs from the eager restore"
         del noise
     del graph, handles
+
+
+@pytest.mark.parametrize("config", [{}, {"pair_launch": False}])
+def test_replays_repack_a_basis_changed_in_place(device, config):
+    """Every replay packs the bases again before its restore launch(es).  The bases are doubled in
+    place between replays; a power of two only moves the block exponents, so each replay must
+    write exactly twice the previous values (a replay that reused the previous fragments or
+    exponents would not)."""
+    jobs, caches = _jobs(device, (96, 160))
+    bases = {job.basis.data_ptr(): job.basis for job in jobs}.values()
+    handle = rk.reconstruct(jobs, config=config)
+    handle.release()
+    torch.cuda.synchronize(device)
+    rk.reserve_capture_staging(1 << 20)  # after the RoPE table's first use, before the capture
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.graph(graph, stream=stream):
+        handles = [rk.reconstruct(jobs, config=config)]
+    torch.cuda.synchronize(device)
+    assert handles[0].stats["variants"] == (["pair"] if not config else ["pairs", "pairs"])
+    graph.replay()
+    torch.cuda.synchronize(device)
+    previous = [cache.float().clone() for cache in caches]
+    assert all(bool(torch.isfinite(p).all()) and float(p.abs().max()) > 0 for p in previous)
+    for replay in range(3):
+        for basis in bases:
+            basis.mul_(2)
+        for cache in caches:
+            cache.fill_(0.0)
+        torch.cuda.synchronize(device)
+        graph.replay()
+        torch.cuda.synchronize(device)
+        for cache, before in zip(caches, previous):
+            assert torch.equal(cache.float(), 2 * before), f"replay {replay + 1} did not repack the doubled bases"
+        previous = [cache.float().clone() for cache in caches]
+    del graph, handles
