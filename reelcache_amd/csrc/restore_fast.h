@@ -65,9 +65,9 @@ struct FastLds {
 // SPLIT = rank halves: 1, or 2 (RCH_GF_SPLIT_RANK, ranks beyond one wave's registers): the
 // workgroup has 8 waves, waves w and w + 4 hold the coefficient fragments of the same 32 tokens
 // for the low and the high half of the rank steps, each computes its half of every block's
-// product, and the two exchange fp32 partial sums through LDS so that each adds them for 8 of
-// the lane's 16 channels and runs their epilogue (the only difference from one chain: the fp32
-// summation order of the two halves).
+// product, and the high half hands its fp32 partial sums to the low half through LDS, which
+// adds them and runs the epilogue (the only difference from one chain: the fp32 summation
+// order of the two halves).
 //
 // One workgroup's part of a launch: work units [first_unit, first_unit + steps) of the tile
 // table (unit u: tile u / (blocks per tile), then dim block and head).
@@ -201,7 +201,7 @@ __device__ __forceinline__ void fast_range(const rch_job* __restrict__ jobs, con
 
     // Tile entry: stage the tile's codes and affine in LDS, convert this wave's 32 tokens to
     // coefficient fragments.  All waves passed a barrier since they last read codes / affine
-    // (rank halves: both halves read partial sums after the step barrier, so the entry starts
+    // (rank halves: the low half reads partial sums after the step barrier, so the entry starts
     // with a barrier of its own).
     auto enter = [&](const rch_job* J, int t0, int first_bp) __attribute__((always_inline)) {
         if constexpr (SPLIT == 2) __syncthreads();
@@ -424,39 +424,6 @@ __device__ __forceinline__ void fast_range(const rch_job* __restrict__ jobs, con
         }
     };
 
-    // Rank halves: the epilogue of 8 of the lane's 16 channels, channels 8 part .. 8 part + 7
-    // (part = the wave's rank half), with the same arithmetic per value as epilogue().
-    auto epilogue_half = [&](const Cursor& c, const float (&sum)[8], const f4 (&rope)[4], int block_e, int part)
-                             __attribute__((always_inline)) {
-        const int e = coef_exp + block_e;
-        float v[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = __builtin_amdgcn_ldexpf(sum[i], -e);
-        if constexpr (ROPE) {
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                const f4 r = part ? rope[2 + q] : rope[q];
-                rotate(v[4 * q], v[4 * q + 1], r[0], r[1]);
-                rotate(v[4 * q + 2], v[4 * q + 3], r[2], r[3]);
-            }
-        }
-        const uint32_t at = dst_lane + static_cast<uint32_t>(c.head * head_bytes + (c.bp * 32 + 8 * part) * kEsize);
-        if constexpr (OUT == RCH_DT_F32) {
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, f4{v[0], v[1], v[2], v[3]}), dst, at, 0, 0);
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, f4{v[4], v[5], v[6], v[7]}), dst, at + 16, 0, 0);
-        } else if constexpr (OUT == RCH_DT_BF16) {
-            bf8 a;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) a[i] = static_cast<__bf16>(v[i]);
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, a), dst, at, 0, 0);
-        } else {
-            h8 a;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) a[i] = static_cast<_Float16>(v[i]);
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, a), dst, at, 0, 0);
-        }
-    };
-
     // One step: products of the staged block(s) over this wave's rank steps, then the epilogue;
     // ends with the step barrier (after which the LDS buffer of this step may be refilled).
     auto finish = [&](const Cursor& c, int buffer, const f4 (&rope)[4]) __attribute__((always_inline)) {
@@ -521,24 +488,20 @@ __device__ __forceinline__ void fast_range(const rch_job* __restrict__ jobs, con
             for (int x = 0; x < HP; ++x) epilogue(c, x, acc[x], rope, block_e[x]);
             __syncthreads();
         } else {
-            // The two halves finish 8 channels each: the low half channels 0-7 of the lane's 16,
-            // the high half channels 8-15.  Each hands the partial sums of the other 8 to its
-            // partner through LDS (lane-contiguous per accumulator element: one 4-byte word per
-            // lane and element, no bank conflicts), so both run the same epilogue and issue the
-            // same stores, and no wave waits for a store it just issued.  Each sum adds the low
-            // half's value and the high half's (fp32 addition commutes: one chain's value either way).
+            // Partial sums of the high half, lane-contiguous per accumulator element (one
+            // 4-byte LDS word per lane and element: no bank conflicts).
             float* partial = reinterpret_cast<float*>(codes) + ((buffer * 4 + group) * 16) * 64 + lane;
-            const int keep_row = 8 * half, send_row = 8 - keep_row;
-            float mine[8];
+            if (half == 1) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                partial[(send_row + i) * 64] = half ? acc[0][i] : acc[0][8 + i];
-                mine[i] = half ? acc[0][8 + i] : acc[0][i];
+                for (int i = 0; i < 16; ++i) partial[i * 64] = acc[0][i];
             }
             __syncthreads();
+            if (half == 0) {
+                f16v sum = acc[0];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) mine[i] += partial[(keep_row + i) * 64];
-            epilogue_half(c, mine, rope, block_e[0], half);
+                for (int i = 0; i < 16; ++i) sum[i] += partial[i * 64];
+                epilogue(c, 0, sum, rope, block_e[0]);
+            }
         }
     };
 
