@@ -56,18 +56,30 @@ def _aligned(x: torch.Tensor, channels: int) -> torch.Tensor:
 def _check_sources(sources) -> tuple[list[torch.Tensor], int, int]:
     if not sources:
         raise ConfigurationError("a fit batch needs at least one matrix")
-    channels = {int(x.shape[1]) for x in sources}
+    shapes = [x.shape for x in sources]  # each tensor's shape, strides and address read once
+    channels = {int(shape[1]) for shape in shapes}
     if len(channels) != 1:
         raise ConfigurationError("one fit batch must share the channel count")
     dtypes = {x.dtype for x in sources}
     if len(dtypes) != 1 or next(iter(dtypes)) not in _DTYPE_CODES:
         raise UnsupportedError("the fit kernels take one of bfloat16, float16 or float32 per batch")
-    for x in sources:
-        if x.ndim != 2 or x.shape[0] < 1 or x.shape[1] < 1:
+    for shape in shapes:
+        if len(shape) != 2 or shape[0] < 1 or shape[1] < 1:
             raise ConfigurationError("fit sources must be nonempty 2-D matrices")
     (c,) = channels
     c8 = padded(c)
-    return [_aligned(x, c8) for x in sources], c, c8
+    if c != c8:
+        return [_aligned(x, c8) for x in sources], c, c8
+    size = sources[0].element_size()
+    aligned = []
+    for x in sources:
+        stride = x.stride()
+        # _aligned's in-place rule (the channel count is c8 here).
+        if stride[1] == 1 and stride[0] >= c8 and (stride[0] * size) % 16 == 0 and x.data_ptr() % 16 == 0:
+            aligned.append(x)
+        else:
+            aligned.append(_aligned(x, c8))
+    return aligned, c, c8
 
 
 def _table(count: int) -> np.ndarray:
@@ -83,9 +95,10 @@ def _upload(table: np.ndarray, device: torch.device) -> torch.Tensor:
 
 
 def _fill_sources(table: np.ndarray, sources) -> None:
-    """Source columns of a descriptor table, filled column by column (not row by row)."""
+    """Source columns of a descriptor table, filled column by column (not row by row); one batch
+    has one dtype (``_check_sources``)."""
     table["src_ptr"] = [x.data_ptr() for x in sources]
-    table["src_dtype"] = [_DTYPE_CODES[x.dtype] for x in sources]
+    table["src_dtype"] = _DTYPE_CODES[sources[0].dtype]
     table["rows"] = [x.shape[0] for x in sources]
     table["src_stride"] = [x.stride(0) for x in sources]
 
@@ -136,11 +149,19 @@ def gram(sources) -> torch.Tensor:
     return grams if c8 == channels else grams[:, :channels, :channels]
 
 
-def _aligned_basis(basis: torch.Tensor, rank: int, c8: int) -> torch.Tensor:
+def _basis_rows(basis: torch.Tensor, rank: int, c8: int, keep: list) -> tuple[int, int]:
+    """(address, row stride) of ``basis[:rank]`` as the kernels read it: the basis itself when its
+    rows can be read in place (``_aligned``'s rule; a row prefix keeps the address and stride), else
+    a zero-padded copy appended to ``keep``."""
     if basis.dtype != torch.float16:
         raise ConfigurationError("the stored basis must be float16")
-    view = basis[:rank]
-    return _aligned(view, c8)
+    stride = basis.stride()
+    address = basis.data_ptr()
+    if basis.shape[1] == c8 and stride[1] == 1 and stride[0] >= c8 and (stride[0] * 2) % 16 == 0 and address % 16 == 0:
+        return address, stride[0]
+    q = _aligned(basis[:rank], c8)
+    keep.append(q)
+    return q.data_ptr(), q.stride(0)
 
 
 def project(sources, bases, ranks, *, extrema: bool = False):
@@ -156,26 +177,29 @@ def project(sources, bases, ranks, *, extrema: bool = False):
     keep, outputs = [], []
     max_rank = max(int(r) for r in ranks)
     keys = torch.zeros((len(aligned), 2 * max_rank), dtype=torch.int32, device=device) if extrema else None
-    strides = [-(-int(rank) // 4) * 4 for rank in ranks]
-    sizes = [int(x.shape[0]) * stride for x, stride in zip(aligned, strides)]
+    ranks = [int(rank) for rank in ranks]
+    rows = [int(x.shape[0]) for x in aligned]
+    strides = [-(-rank // 4) * 4 for rank in ranks]
+    sizes = [count * stride for count, stride in zip(rows, strides)]
     storage = torch.empty(sum(sizes), dtype=torch.float32, device=device)  # every P of the batch, 16-byte rows
+    storage_address = storage.data_ptr()
     first = 0
-    columns = {"basis_ptr": [], "basis_stride": [], "rank": [], "coef_ptr": []}
-    for index, (x, basis, rank) in enumerate(zip(aligned, bases, ranks)):
-        rank = int(rank)
-        if not 1 <= rank <= basis.shape[0] or basis.shape[1] > c8 or basis.device != device:
+    basis_ptr, basis_stride, coef_ptr = [], [], []
+    for index, (basis, rank) in enumerate(zip(bases, ranks)):
+        shape = basis.shape
+        if not 1 <= rank <= shape[0] or shape[1] > c8 or basis.device != device:
             raise ConfigurationError("projection basis does not match its source")
-        q = _aligned_basis(basis, rank, c8)
-        p = storage[first:first + sizes[index]].view(int(x.shape[0]), strides[index])
+        address, stride = _basis_rows(basis, rank, c8, keep)
+        basis_ptr.append(address)
+        basis_stride.append(stride)
+        # P of source index: rows x stride fp32 at element offset `first` of the storage.
+        outputs.append(torch.as_strided(storage, (rows[index], rank), (strides[index], 1), first))
+        coef_ptr.append(storage_address + 4 * first)
         first += sizes[index]
-        keep.append(q)
-        outputs.append(p[:, :rank])
-        columns["basis_ptr"].append(q.data_ptr())
-        columns["basis_stride"].append(q.stride(0))
-        columns["rank"].append(rank)
-        columns["coef_ptr"].append(p.data_ptr())
-    for name, values in columns.items():
-        table[name] = values
+    table["basis_ptr"] = basis_ptr
+    table["basis_stride"] = basis_stride
+    table["rank"] = ranks
+    table["coef_ptr"] = coef_ptr
     table["coef_stride"] = strides
     if extrema:
         table["extrema_ptr"] = keys.data_ptr() + 4 * 2 * max_rank * np.arange(len(aligned))
@@ -243,16 +267,20 @@ def energies(sources, absmax_keys: torch.Tensor, *, bases=None, ranks=None, coef
             rank = int(rank)
             if not 1 <= rank <= basis.shape[0] or p.shape != (x.shape[0], rank) or p.dtype != torch.float32:
                 raise ConfigurationError("residual coefficients do not match their source and rank")
-            q = _aligned_basis(basis, rank, c8)
-            if p.stride(1) != 1 or (p.stride(0) * 4) % 16 or p.data_ptr() % 16:
+            basis_address, basis_stride = _basis_rows(basis, rank, c8, keep)
+            p_stride = p.stride()
+            p_address = p.data_ptr()
+            if p_stride[1] != 1 or (p_stride[0] * 4) % 16 or p_address % 16:
                 stride = -(-rank // 4) * 4
                 copy = torch.zeros((p.shape[0], stride), dtype=torch.float32, device=device)
                 copy[:, :rank].copy_(p)
-                p = copy
-            keep += [q, p]
-            for name, value in (("basis_ptr", q.data_ptr()), ("basis_stride", q.stride(0)), ("rank", rank),
-                                ("coef_ptr", p.data_ptr()), ("coef_stride", p.stride(0))):
-                columns[name].append(value)
+                keep.append(copy)
+                p_stride, p_address = copy.stride(), copy.data_ptr()
+            columns["basis_ptr"].append(basis_address)
+            columns["basis_stride"].append(basis_stride)
+            columns["rank"].append(rank)
+            columns["coef_ptr"].append(p_address)
+            columns["coef_stride"].append(p_stride[0])
         for name, values in columns.items():
             table[name] = values
     descriptors = _upload(table, device)
