@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-#define RCH_ABI_VERSION 11
+#define RCH_ABI_VERSION 12
 
 /* Status codes (mapped to reelcache errors by the host). */
 #define RCH_OK 0
@@ -158,7 +158,6 @@ typedef struct rch_pack {
 int rch_abi_version(void);
 int rch_job_size(void);
 int rch_pack_size(void);
-int rch_slice_entry_size(void);
 const char* rch_last_error(void);
 /* Size in bytes of one packed fragment for a precision (16 or 32). */
 int rch_fragment_bytes(int precision);
@@ -236,47 +235,6 @@ int rch_restore_pair(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_d
  */
 int rch_restore_pair_occupancy(int precision, int source_kind, int ksteps0, int ksteps1, int head_dim, int out_dtype,
                                int* blocks_per_cu);
-
-/*
- * One entry of a channel-slice restore launch: 32-token tiles [tile0 + u0, tile0 + u1) of one
- * (basis, head slice) pair; every tile is computed for all of the slice's heads.  The tiles of
- * an entry belong to at most 8 distinct jobs.
- */
-typedef struct rch_slice_entry {
-    int32_t tile0;       /* first 32-token tile (index into the tile table) of the pair's jobs */
-    int32_t head0, nh;   /* the slice's heads; ceil(nh / 2) * 2 * head_dim / 32 <= the slice blocks */
-    int32_t u0, u1;      /* tile range of this entry, relative to tile0 */
-    int32_t pack_job;    /* a job of the pair: its pack_ptr / pack_nblocks / basis_exp_index give the basis */
-    int32_t pack_ksteps; /* 16-row steps held by that pack */
-    int32_t reserved;
-} rch_slice_entry;       /* 8 x int32 = 32 bytes */
-
-/*
- * 32-channel blocks one channel-slice workgroup computes per tile (0 when no slice variant is
- * compiled for these arguments; a slice holds at most that many blocks, in pairs of heads) and
- * its resident workgroups per CU (sizes the grid).  Same role as rch_restore_occupancy for
- * rch_restore_sliced.
- */
-int rch_restore_slice_blocks(int precision, int max_ksteps, int out_dtype, int group_flags, int* max_blocks,
-                             int* blocks_per_cu);
-
-/*
- * The fused restore of rch_restore (same arithmetic, identical values) organised by head
- * slice: workgroups of 4 waves (two per CU) walk 32-token tiles in lockstep, each wave holding
- * the basis fragments of two blocks in registers; each tile is dequantized once per workgroup
- * into LDS.  Workgroup w processes entries [wg_entries[w'], wg_entries[w' + 1])
- * (w' = XCD-swizzled index).  For launch groups flagged RCH_GF_FAST whose jobs all have uint8
- * codes in 16-byte aligned rows (RCH_JF_SRC_VEC, no pictures), fp16 / fp16x2 / bf16 products,
- * head_dim % 32 == 0 and channels == heads * head_dim.
- *   tiles_dev int32 [n_tiles, 2]: (job, first token) of every 32-token tile, the tiles of the
- *             jobs sharing a pack contiguous.
- * Replaces _fused_restore_kernel / _fused_group (reelcache/restore_kernels.py:1447-1515,
- * :2025-2098) for those groups.
- */
-int rch_restore_sliced(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev, int n_tiles,
-                       const rch_slice_entry* entries_dev, int n_entries, const int32_t* wg_entries_dev, int grid,
-                       int channels, int head_dim, int out_dtype, int precision, int max_ksteps, int group_flags,
-                       const int32_t* scratch_dev, void* stream);
 
 /*
  * rch_basis_pack + rch_restore of one launch group that allocates nothing: the packed bases and

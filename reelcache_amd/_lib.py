@@ -16,7 +16,7 @@ import numpy as np
 from .errors import ConfigurationError, UnsupportedError
 
 LIBRARY = Path(__file__).resolve().with_name("libreelcache_hip.so")
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 # Status codes (RCH_E_*).
 OK, E_CONFIG, E_UNSUPPORTED, E_LAUNCH = 0, 1, 2, 3
@@ -61,9 +61,6 @@ QUANTIZE_FIELDS = ("values_ptr", "rows", "cols", "stride", "affine_ptr", "codes_
 QUANTIZE_DTYPE = np.dtype([(name, "<i8") for name in QUANTIZE_FIELDS])
 GAUSS_FIELDS = ("dst_ptr", "rows", "cols", "stride", "seed", "reserved0", "reserved1", "reserved2")
 GAUSS_DTYPE = np.dtype([(name, "<i8") for name in GAUSS_FIELDS])
-# rch_slice_entry field order (8 x int32).
-SLICE_ENTRY_FIELDS = ("tile0", "head0", "nh", "u0", "u1", "pack_job", "pack_ksteps", "reserved")
-SLICE_ENTRY_DTYPE = np.dtype([(name, "<i4") for name in SLICE_ENTRY_FIELDS])
 
 _i, _i64, _p = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
 _SIGNATURES = {
@@ -78,9 +75,6 @@ _SIGNATURES = {
     "rch_restore_occupancy": ([_i, _i, _i, _i, _i, _i, ctypes.POINTER(_i)], _i),
     "rch_restore_pair": ([_p, _i, _p, _i, _i, _p, _i, _i, _i, _i, _i, _i, _i, _i, _p, _p], _i),
     "rch_restore_pair_occupancy": ([_i, _i, _i, _i, _i, _i, ctypes.POINTER(_i)], _i),
-    "rch_slice_entry_size": ([], _i),
-    "rch_restore_slice_blocks": ([_i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i)], _i),
-    "rch_restore_sliced": ([_p, _i, _p, _i, _p, _i, _p, _i, _i, _i, _i, _i, _i, _i, _p, _p], _i),
     "rch_rope_store": ([_p, _i, _p, _i, _i, _i, _i, _p], _i),
     "rch_staged_unpack": ([_p, _i, _p, _i, _p, _p, _i64, _i, _i, _i, _i, _p, _p], _i),
     "rch_staged_store": ([_p, _i, _p, _i, _p, _p, _i64, _i, _i, _i, _i, _p, _p], _i),
@@ -124,8 +118,7 @@ def _load():
     if lib.rch_abi_version() != ABI_VERSION:
         raise UnsupportedError(f"{LIBRARY.name} has ABI {lib.rch_abi_version()}, expected {ABI_VERSION}; rebuild it")
     if (lib.rch_job_size() != JOB_DTYPE.itemsize or lib.rch_pack_size() != PACK_DTYPE.itemsize
-            or lib.rch_fit_matrix_size() != FIT_DTYPE.itemsize
-            or lib.rch_slice_entry_size() != SLICE_ENTRY_DTYPE.itemsize):
+            or lib.rch_fit_matrix_size() != FIT_DTYPE.itemsize):
         raise UnsupportedError(f"{LIBRARY.name} descriptor layout differs from this package; rebuild it")
     return lib
 
@@ -201,10 +194,3 @@ def pair_occupancy(precision: int, source_kind: int, ksteps0: int, ksteps1: int,
     return blocks.value
 
 
-def slice_blocks(precision: int, max_ksteps: int, out_dtype: int, group_flags: int) -> tuple[int, int]:
-    """(32-channel blocks one channel-slice workgroup computes, resident workgroups per CU);
-    (0, 0) when no slice variant is compiled for these arguments."""
-    blocks, per_cu = ctypes.c_int(0), ctypes.c_int(0)
-    call("rch_restore_slice_blocks", precision, max_ksteps, out_dtype, group_flags, ctypes.byref(blocks),
-         ctypes.byref(per_cu))
-    return blocks.value, per_cu.value

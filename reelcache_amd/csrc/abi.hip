@@ -29,7 +29,6 @@ extern "C" {
 int rch_abi_version(void) { return RCH_ABI_VERSION; }
 int rch_job_size(void) { return static_cast<int>(sizeof(rch_job)); }
 int rch_pack_size(void) { return static_cast<int>(sizeof(rch_pack)); }
-int rch_slice_entry_size(void) { return static_cast<int>(sizeof(rch_slice_entry)); }
 const char* rch_last_error(void) { return rch::g_last_error; }
 
 }  // extern "C"

@@ -5,7 +5,7 @@
 // :1557-1585, _fused_group / _two_pass_group :2025-2121).
 #include <mutex>
 
-#include "restore_slice.h"
+#include "restore_fast.h"
 #include "restore_stream.h"
 
 namespace rch {
@@ -690,53 +690,6 @@ int rch_restore_pair(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_d
     hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, as_stream(stream), jobs_dev,
                        tiles_dev, bounds_dev, scratch_dev, int64_t(0), heads, head_dim, split_unit);
     return check_launch("rch_restore_pair");
-}
-
-// The channel-slice kernel (restore_slice.h) for a group, or nullptr when none is compiled for
-// its rank / output / precision.
-static SliceFn pick_slice_launch(int precision, int max_ksteps, int out_dtype, int group_flags, int* max_blocks) {
-    const bool rope = (group_flags & RCH_GF_ROPE) != 0;
-    int ks = 0;
-    *max_blocks = 0;
-    if (!(group_flags & RCH_GF_FAST) || max_ksteps <= 0) return nullptr;
-    switch (precision) {
-        case RCH_PREC_FP16: return pick_slice_fp16(max_ksteps, rope, out_dtype, &ks, max_blocks);
-        case RCH_PREC_FP16X2: return pick_slice_fp16x2(max_ksteps, rope, out_dtype, &ks, max_blocks);
-        case RCH_PREC_BF16: return pick_slice_bf16(max_ksteps, rope, out_dtype, &ks, max_blocks);
-        default: return nullptr;
-    }
-}
-
-int rch_restore_slice_blocks(int precision, int max_ksteps, int out_dtype, int group_flags, int* max_blocks,
-                             int* blocks_per_cu) {
-    if (!max_blocks || !blocks_per_cu) return fail(RCH_E_CONFIG, "rch_restore_slice_blocks: invalid arguments");
-    *blocks_per_cu = 0;
-    SliceFn fn = pick_slice_launch(precision, max_ksteps, out_dtype, group_flags, max_blocks);
-    if (!fn) return RCH_OK;
-    const hipError_t error = hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, fn, kSliceThreads, 0);
-    if (error != hipSuccess)
-        return fail(RCH_E_LAUNCH, "rch_restore_slice_blocks: %s", hipGetErrorString(error));
-    return RCH_OK;
-}
-
-int rch_restore_sliced(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev, int n_tiles,
-                       const rch_slice_entry* entries_dev, int n_entries, const int32_t* wg_entries_dev, int grid,
-                       int channels, int head_dim, int out_dtype, int precision, int max_ksteps, int group_flags,
-                       const int32_t* scratch_dev, void* stream) {
-    if (!jobs_dev || !tiles_dev || !entries_dev || !wg_entries_dev || !scratch_dev || n_jobs <= 0 || n_tiles <= 0 ||
-        n_entries <= 0 || grid <= 0 || channels <= 0 || head_dim <= 0 || head_dim % 32 || channels % head_dim ||
-        max_ksteps <= 0)
-        return fail(RCH_E_CONFIG, "rch_restore_sliced: invalid launch arguments");
-    if (!valid_out(out_dtype)) return fail(RCH_E_CONFIG, "rch_restore_sliced: output dtype must be f32, f16 or bf16");
-    int max_blocks = 0;
-    SliceFn fn = pick_slice_launch(precision, max_ksteps, out_dtype, group_flags, &max_blocks);
-    if (!fn) return fail(RCH_E_UNSUPPORTED, "rch_restore_sliced: no slice variant for this precision / rank / flags");
-    if (max_blocks < head_dim / 32)
-        return fail(RCH_E_UNSUPPORTED, "rch_restore_sliced: one head's basis fragments exceed the LDS");
-    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(grid)), dim3(kSliceThreads), 0, as_stream(stream), jobs_dev,
-                       tiles_dev, entries_dev, wg_entries_dev, scratch_dev,
-                       head_dim);
-    return check_launch("rch_restore_sliced");
 }
 
 int rch_rope_store(const rch_job* jobs_dev, int n_jobs, const int32_t* tiles_dev, int n_tiles, int channels,

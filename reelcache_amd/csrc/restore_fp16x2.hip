@@ -1,5 +1,5 @@
 // fp16x2 variants of the fused restore kernel (one translation unit per precision).
-#include "restore_slice.h"
+#include "restore_fast.h"
 
 namespace rch {
 
@@ -9,8 +9,5 @@ FastFn pick_fast_fp16x2(int ks, bool rope, int out_dtype, int shape, int* chosen
     return pick_fast<RCH_PREC_FP16X2>(ks, rope, out_dtype, shape, chosen);
 }
 
-SliceFn pick_slice_fp16x2(int ks, bool rope, int out_dtype, int* chosen, int* max_blocks) {
-    return pick_slice<RCH_PREC_FP16X2>(ks, rope, out_dtype, chosen, max_blocks);
-}
 
 }  // namespace rch

@@ -60,11 +60,11 @@ from .errors import ConfigurationError, UnsupportedError
 from .restore_handle import RestoreHandle, _sweep_deferred, park_failed, pending_deferred
 from .restore_model import (COEFFICIENT_DTYPES, LAYOUTS, OUTPUT_DTYPES, CoefficientSource, DenseSource, NativeView,
                             PictureSource, ReconstructionJob, RopePositions, RopeTable, expand_affine, wan_sections)
-from .restore_plan import (DEFAULT_MERGED, _DEFAULT_CONFIG, _RETIRED_SLABS, _STAGING, BASIS_DTYPES, SLICE_JOBS,  # noqa: F401
-                           SLICE_TOKENS, STAGED_PRECISIONS, STREAM_TOKENS, TILE_TOKENS, _balanced_bounds,
+from .restore_plan import (DEFAULT_MERGED, _DEFAULT_CONFIG, _RETIRED_SLABS, _STAGING, BASIS_DTYPES,  # noqa: F401
+                           STAGED_PRECISIONS, STREAM_TOKENS, TILE_TOKENS, _balanced_bounds,
                            _capture_staging, check_staged_precision, staged_gemm,
                            _coefficient_bound, _fast_flags, _pinned_bytes, _prescale_exponent,
-                           _slice_heads, _slice_plan, _tiles, job_desc, reserve_capture_staging, run_call)
+                           _tiles, job_desc, reserve_capture_staging, run_call)
 from .restore_reference import (_OUTPUT_FLOOR, _UNIT_ROUNDOFF, _check_compute_dtype,  # noqa: F401
                                 _check_disjoint, _facts, _gemm_gamma, _native_rotation, _require_fp32_matmul, _storage_key,
                                 _validate, apply_rope_reference, dequantize, error_bound, fp32_matmul_precision,

@@ -31,10 +31,9 @@ from .restore_model import CoefficientSource, DenseSource, PictureSource, settle
 from .restore_reference import _require_fp32_matmul
 
 TILE_TOKENS = 128  # tokens per workgroup tile (4 waves x 32)
-SLICE_TOKENS = 32  # tokens per tile of the channel-slice kernel (one wave's MFMA columns)
 BASIS_DTYPES = (torch.float16, torch.bfloat16)
 _DEFAULT_CONFIG = {"TILE_TOKENS": TILE_TOKENS, "BLOCK_N": 32, "waves": 4, "workgroups_per_cu": None,
-                   "store_cost": None, "fast_variant": True, "slice_variant": False, "head_pairs": True,
+                   "store_cost": None, "fast_variant": True, "head_pairs": True,
                    "split_rank": True, "static_scratch": False, "stream_variant": False,
                    "pair_launch": True}
 DEFAULT_MERGED = dict(_DEFAULT_CONFIG)  # the merged configuration of calls without overrides (never modified)
@@ -195,109 +194,6 @@ def _tiles(job_indices, jobs, size=TILE_TOKENS):
     tiles[:, 0] = np.repeat(np.asarray(job_indices, dtype=np.int32), counts)
     tiles[:, 1] = (np.arange(total, dtype=np.int64) - first) * size
     return tiles
-
-
-_SLICE_BLOCKS: dict = {}
-
-
-def _slice_blocks(code, max_ksteps, out_dtype, group_flags):
-    """(32-channel blocks one channel-slice workgroup computes, workgroups per CU) of a variant
-    ((0, 0): no slice variant)."""
-    key = (code, max_ksteps, out_dtype, group_flags)
-    if key not in _SLICE_BLOCKS:
-        _SLICE_BLOCKS[key] = _lib.slice_blocks(code, max_ksteps, out_dtype, group_flags)
-    return _SLICE_BLOCKS[key]
-
-
-SLICE_JOBS = 8  # jobs whose affine one channel-slice entry stages (csrc/restore_slice.h kSliceJobs)
-
-
-def _slice_heads(blocks, head_blocks):
-    """Heads per slice for a slice workgroup holding ``blocks`` 32-channel blocks: pairs of heads
-    (one dim block of two heads per wave), so an even count unless one head is all that fits;
-    0 when not even two heads' blocks fit."""
-    if head_blocks < 1 or 2 * head_blocks > blocks:
-        return 0
-    heads = blocks // head_blocks
-    return heads - (heads & 1)
-
-
-def _slice_plan(members, jobs, member_packs, pack_steps, heads, head_blocks, heads_per_slice, grid):
-    """Work of one channel-slice launch (csrc/restore_slice.h): ``(tiles, entries, wg_entries)``.
-
-    The group's jobs are ordered so that jobs sharing a basis pack are contiguous (one segment
-    per pack) and cut into 32-token tiles.  The heads are split into near-equal slices of at
-    most ``heads_per_slice``; a (segment, slice) pair is one tile per segment tile, every tile
-    of equal cost (a workgroup computes all of its slice's blocks per tile).  The concatenated
-    tiles of all pairs are split into ``grid`` near-equal ranges, each range into one entry per
-    pair it touches, and entries touching more than ``SLICE_JOBS`` jobs are split further."""
-    order = sorted(range(len(members)), key=lambda position: member_packs[position])
-    ordered = [members[position] for position in order]
-    packs = [member_packs[position] for position in order]
-    tiles = _tiles(ordered, jobs, SLICE_TOKENS)
-    counts = np.array([(jobs[index].tokens + SLICE_TOKENS - 1) // SLICE_TOKENS for index in ordered], np.int64)
-    # Ordinal of each tile's job in the ordered list (jobs of one entry = an ordinal range).
-    job_ordinal = np.repeat(np.arange(len(ordered), dtype=np.int64), counts)
-    seg_tile0, seg_tiles, seg_job, seg_steps = [], [], [], []
-    start = 0
-    for position, index in enumerate(ordered):
-        if position == 0 or packs[position] != packs[position - 1]:
-            seg_tile0.append(start)
-            seg_tiles.append(0)
-            seg_job.append(index)
-            seg_steps.append(pack_steps[packs[position]])
-        seg_tiles[-1] += int(counts[position])
-        start += int(counts[position])
-    n_slices = -(-heads // heads_per_slice)
-    sizes = np.array([heads // n_slices + (1 if s < heads % n_slices else 0) for s in range(n_slices)], np.int64)
-    first_head = np.concatenate(([0], np.cumsum(sizes)[:-1]))
-    segments = len(seg_tile0)
-    pair_tile0 = np.repeat(np.asarray(seg_tile0, np.int64), n_slices)
-    pair_units = np.repeat(np.asarray(seg_tiles, np.int64), n_slices)
-    starts = np.concatenate(([0], np.cumsum(pair_units)))
-    total = int(starts[-1])
-    if total > 2 ** 31 - 1:
-        raise UnsupportedError("restore launch group exceeds 2**31 tiles; split the call")
-    bounds = np.rint(total * np.arange(grid + 1, dtype=np.float64) / grid).astype(np.int64)
-    cuts = np.unique(np.concatenate((starts, bounds)))
-    low, high = cuts[:-1], cuts[1:]
-    pair = np.searchsorted(starts, low, side="right") - 1
-    # Entries touching more than SLICE_JOBS jobs are cut at job boundaries (rare: tiny jobs).
-    first_tile = pair_tile0[pair] + low - starts[pair]
-    last_tile = pair_tile0[pair] + high - starts[pair] - 1
-    if bool((job_ordinal[last_tile] - job_ordinal[first_tile] >= SLICE_JOBS).any()):
-        extra = []
-        for lo, hi, p, a, b in zip(low.tolist(), high.tolist(), pair.tolist(), first_tile.tolist(), last_tile.tolist()):
-            if job_ordinal[b] - job_ordinal[a] < SLICE_JOBS:
-                continue
-            tile = a
-            while True:
-                limit = int(np.searchsorted(job_ordinal, job_ordinal[tile] + SLICE_JOBS, side="left"))
-                if limit > b:
-                    break
-                extra.append(lo + limit - a)
-                tile = limit
-        cuts = np.unique(np.concatenate((cuts, np.asarray(extra, np.int64))))
-        low, high = cuts[:-1], cuts[1:]
-        pair = np.searchsorted(starts, low, side="right") - 1
-    owner = np.searchsorted(bounds, low, side="right") - 1
-    entries = np.zeros(len(low), dtype=_lib.SLICE_ENTRY_DTYPE)
-    entries["tile0"] = pair_tile0[pair]
-    entries["head0"] = np.tile(first_head, segments)[pair]
-    entries["nh"] = np.tile(sizes, segments)[pair]
-    entries["u0"] = low - starts[pair]
-    entries["u1"] = high - starts[pair]
-    entries["pack_job"] = np.repeat(np.asarray(seg_job, np.int64), n_slices)[pair]
-    entries["pack_ksteps"] = np.repeat(np.asarray(seg_steps, np.int64), n_slices)[pair]
-    wg_entries = np.searchsorted(owner, np.arange(grid + 1), side="left").astype(np.int32)
-    # The kernel trusts these tables: every entry inside its pair, every tile inside the table,
-    # at most SLICE_JOBS jobs per entry, slices of whole head pairs within the workgroup's blocks.
-    a = entries["tile0"].astype(np.int64) + entries["u0"]
-    b = entries["tile0"].astype(np.int64) + entries["u1"] - 1
-    assert bool((entries["u1"] <= pair_units[pair]).all() and (entries["u0"] < entries["u1"]).all())
-    assert int(b.max()) < len(tiles) and bool((job_ordinal[b] - job_ordinal[a] < SLICE_JOBS).all())
-    assert int(entries["nh"].max()) <= heads_per_slice and wg_entries[-1] == len(entries)
-    return tiles, entries, wg_entries
 
 
 _JOB_INDEX = {name: index for index, name in enumerate(_lib.JOB_FIELDS)}
@@ -607,7 +503,6 @@ class _Layout:
             raise ConfigurationError("static_scratch restores hold no device coefficient bounds: float sources in "
                                      "the fp16 modes need a host bound")
         allow_fast = bool(_config_value(config, "fast_variant"))
-        allow_slice = allow_fast and bool(_config_value(config, "slice_variant")) and not self.static
         allow_pairs = allow_fast and bool(_config_value(config, "head_pairs"))
         allow_split = bool(_config_value(config, "split_rank"))
         allow_stream = allow_fast and bool(_config_value(config, "stream_variant")) and precision == "fp16x2"
@@ -651,17 +546,6 @@ class _Layout:
             if stream:
                 self._stream_plan(descs, plan, stream_flags, compute_units, arena)
                 continue
-            if allow_slice and kind == _lib.SRC_U8 and group_flags & _lib.GF_FAST:
-                head_blocks = head_dim // 32
-                blocks, slice_per_cu = _slice_blocks(self.code, max_ksteps, plan["out_dtype"], group_flags)
-                per_slice = _slice_heads(blocks, head_blocks)
-                if per_slice >= 1 and slice_per_cu >= 1:
-                    slice_grid = compute_units * slice_per_cu
-                    plan["pending_slice"] = (group_flags, head_blocks, per_slice, slice_grid)
-                    plan.update(variant="sliced", flags=group_flags, grid=slice_grid)
-                    self.grids.append(slice_grid)
-                    self.variants.append("sliced")
-                    continue
             tiles = _tiles(members, descs)
             if group_flags & _lib.GF_FAST and max_ksteps > _FAST_MAX_KSTEPS[precision]:
                 # Beyond one wave's registers: rank halves in 8-wave workgroups (uint8 rows, up to
@@ -782,8 +666,7 @@ class _Layout:
 
     def _packs(self, descs, plans, basis_groups, arena):
         """The basis packs: one per job of a stream group (its scaled slabs), one per distinct basis
-        view for the other kernels (fragments of the largest rank used); then the pending work
-        tables of channel-slice groups, which index packs."""
+        view for the other kernels (fragments of the largest rank used)."""
         packs: list = []
         pack_of: dict = {}
         by_basis: dict = {}
@@ -816,18 +699,6 @@ class _Layout:
         for pack in packs:
             if pack["kind"] == _lib.PACK_FRAGMENTS:
                 pack["ksteps"] = (pack["rank"] + 15) // 16
-        for plan in plans:
-            pending = plan.pop("pending_slice", None)
-            if pending is None:
-                continue
-            group_flags, head_blocks, per_slice, slice_grid = pending
-            members = plan["members"]
-            ksteps = [pack["ksteps"] for pack in packs]
-            tiles, entries, wg_entries = _slice_plan(members, descs, [pack_of[i] for i in members], ksteps,
-                                                     plan["channels"] // plan["head_dim"], head_blocks, per_slice,
-                                                     slice_grid)
-            plan.update(tiles=arena.add(tiles), n_tiles=len(tiles), entries=arena.add(entries),
-                        n_entries=len(entries), bounds=arena.add(wg_entries))
         return packs, pack_of
 
     def _pack_layout(self, descs, rows, relative, plans, packs, pack_of):
@@ -942,10 +813,6 @@ class _Layout:
             if variant == "dense":
                 _lib.call("rch_rope_store", table, jobs, base + plan["tiles"], plan["n_tiles"], plan["channels"],
                           plan["head_dim"], plan["out_dtype"], hip_stream)
-            elif variant == "sliced":
-                _lib.call("rch_restore_sliced", table, jobs, base + plan["tiles"], plan["n_tiles"], base + plan["entries"],
-                          plan["n_entries"], base + plan["bounds"], plan["grid"], plan["channels"], plan["head_dim"],
-                          plan["out_dtype"], self.code, plan["max_ksteps"], plan["flags"], scratch_base, hip_stream)
             elif variant == "pair":
                 _lib.call("rch_restore_pair", table, jobs, base + plan["tiles"], plan["n_tiles0"], plan["n_tiles1"],
                           base + plan["bounds"], plan["grid"], plan["channels"], plan["head_dim"], plan["kind"],

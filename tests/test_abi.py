@@ -31,13 +31,12 @@ def test_abi_version_and_descriptor_layout():
     assert lib.rch_fragment_bytes(_lib.PRECISION_CODES["fp32"]) == 32
     assert lib.rch_fit_matrix_size() == _lib.FIT_DTYPE.itemsize == 16 * 8
     assert _lib.QUANTIZE_DTYPE.itemsize == 8 * 8
-    assert lib.rch_slice_entry_size() == _lib.SLICE_ENTRY_DTYPE.itemsize == 8 * 4
 
 
 def test_header_struct_fields_match_the_binding():
-    """Field order of the int64 / int32 descriptor structs in the header == the numpy dtypes."""
+    """Field order of the int64 descriptor structs in the header == the numpy dtypes."""
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    for struct, fields in (("rch_job", _lib.JOB_FIELDS), ("rch_slice_entry", _lib.SLICE_ENTRY_FIELDS)):
+    for struct, fields in (("rch_job", _lib.JOB_FIELDS), ("rch_pack", _lib.PACK_FIELDS)):
         body = re.search(r"typedef struct " + struct + r" \{(.*?)\}", text, flags=re.S).group(1)
         names = []
         for declaration in body.split(";"):

@@ -38,7 +38,7 @@ def _jobs(device, ranks=(96, 160)):
 
 
 @pytest.mark.parametrize("config,ranks", [({}, (96, 160)), ({"head_pairs": False}, (96, 160)),
-                                          ({"slice_variant": True}, (96, 160)), ({"fast_variant": False}, (96, 160)),
+                                          ({"fast_variant": False}, (96, 160)),
                                           ({}, (256, 448)),  # rank halves (8-wave workgroups)
                                           ({"stream_variant": True}, (96, 160)),  # the stream kernel
                                           ({"stream_variant": True, "static_scratch": True}, (96, 160)),

@@ -182,65 +182,6 @@ def test_balanced_bounds_partition_the_units(grid):
         assert per_range.max() <= unit_cost.sum() / grid + unit_cost.max() + 1e-9
 
 
-def _walk_slice_plan(tiles, entries, wg_entries, head_blocks):
-    """The channel-slice kernel's decomposition (csrc/restore_slice.h) replayed on the host:
-    every (job, first token, head, dim block, pack job) unit it computes.  A workgroup computes
-    every tile of each of its entries for all of the slice's heads and dim blocks."""
-    done = []
-    for wg in range(len(wg_entries) - 1):
-        for entry in entries[wg_entries[wg]:wg_entries[wg + 1]]:
-            for tile in range(int(entry["tile0"] + entry["u0"]), int(entry["tile0"] + entry["u1"])):
-                job, token = tiles[tile]
-                for head in range(int(entry["head0"]), int(entry["head0"] + entry["nh"])):
-                    for bp in range(head_blocks):
-                        done.append((int(job), int(token), head, bp, int(entry["pack_job"])))
-    return done
-
-
-def test_slice_heads_are_pairs_within_the_workgroup():
-    assert rk._slice_heads(16, 4) == 4 and rk._slice_heads(16, 2) == 8 and rk._slice_heads(16, 8) == 2
-    assert rk._slice_heads(16, 3) == 4  # 5 heads fit, slices hold pairs
-    assert rk._slice_heads(16, 9) == 0 and rk._slice_heads(0, 4) == 0
-
-
-@pytest.mark.parametrize("heads,head_blocks,per_slice,grid", [(12, 4, 4, 256), (12, 4, 2, 256), (5, 3, 4, 7),
-                                                              (32, 4, 4, 256), (1, 2, 8, 3), (13, 2, 8, 64)])
-def test_slice_plan_covers_every_unit_once(heads, head_blocks, per_slice, grid):
-    # Jobs over three bases (packs 0, 2, 1 interleaved), ragged token counts.
-    jobs = [_Job(t) for t in (4680, 31, 33, 1, 700, 4680, 64)]
-    members = [0, 1, 2, 3, 4, 5, 6]
-    packs = [0, 2, 0, 1, 2, 0, 1]
-    steps = [12, 8, 4]
-    tiles, entries, wg_entries = rk._slice_plan(members, jobs, packs, steps, heads, head_blocks, per_slice, grid)
-    assert tiles.dtype == np.int32 and entries.dtype == _lib.SLICE_ENTRY_DTYPE and wg_entries.shape == (grid + 1,)
-    done = _walk_slice_plan(tiles, entries, wg_entries, head_blocks)
-    expected = {(j, t, head, bp) for j in members for t in range(0, jobs[j].tokens, 32)
-                for head in range(heads) for bp in range(head_blocks)}
-    assert len(done) == len(expected) and {unit[:4] for unit in done} == expected
-    for job, _, _, _, pack_job in done:  # the slice's basis is the job's own pack
-        assert packs[members.index(pack_job)] == packs[members.index(job)]
-    assert int(entries["nh"].max()) <= per_slice
-    assert all(steps[packs[members.index(int(e["pack_job"]))]] == e["pack_ksteps"] for e in entries)
-    for entry in entries:  # at most SLICE_JOBS jobs per entry
-        span = tiles[int(entry["tile0"] + entry["u0"]):int(entry["tile0"] + entry["u1"]), 0]
-        assert len(set(span.tolist())) <= rk.SLICE_JOBS
-    # Near-equal tiles per workgroup (tiles are equal-cost).
-    per_wg = np.zeros(grid)
-    for wg in range(grid):
-        for entry in entries[wg_entries[wg]:wg_entries[wg + 1]]:
-            per_wg[wg] += entry["u1"] - entry["u0"]
-    assert per_wg.max() - per_wg.min() <= 1
-
-
-def test_slice_plan_splits_entries_over_many_small_jobs():
-    jobs = [_Job(32) for _ in range(40)]  # one tile each: a workgroup range touches many jobs
-    tiles, entries, wg_entries = rk._slice_plan(list(range(40)), jobs, [0] * 40, [4], 4, 4, 4, 2)
-    done = _walk_slice_plan(tiles, entries, wg_entries, 4)
-    assert len(done) == 40 * 4 * 4 and len(set(done)) == len(done)
-    for entry in entries:
-        assert entry["u1"] - entry["u0"] <= rk.SLICE_JOBS
-
-
 def test_fast_eligibility_rules():
     rng = np.random.default_rng(27)
     case = make_case(rng, grid=(1, 4, 8), heads=2, head_dim=64, rank=32, rope="none")

@@ -1,11 +1,9 @@
-"""GPU parity of the straight-line and channel-slice restore kernels (csrc/restore_fast.h,
-csrc/restore_slice.h).
+"""GPU parity of the straight-line restore kernels (csrc/restore_fast.h).
 
 Launch groups whose jobs all qualify (uint8 codes in 16-byte aligned rows or pictures,
 head_dim % 32 == 0, unit-stride aligned destinations) run the straight-line kernel (two heads
-per step when the head count is even, one with ``config={"head_pairs": False}``), or, with
-``config={"slice_variant": True}``, the channel-slice kernel (uint8 rows); every case here runs
-the same inputs through the straight-line, channel-slice and general kernels
+per step when the head count is even, one with ``config={"head_pairs": False}``); every case
+here runs the same inputs through the straight-line and general kernels
 (``config={"fast_variant": False}``) and requires equal values, then checks them against the
 oracle's elementwise error bound (reelcache/restore_kernels.py:1208-1227).
 """
@@ -34,8 +32,7 @@ SHAPES = [
 ]
 
 
-VARIANTS = {"sliced": {"slice_variant": True}, "pairs": {}, "fast": {"head_pairs": False},
-            "general": {"fast_variant": False}}
+VARIANTS = {"pairs": {}, "fast": {"head_pairs": False}, "general": {"fast_variant": False}}
 
 
 def _copies(seed, precision, out_dtype, shape, device, count=len(VARIANTS)):
@@ -71,12 +68,12 @@ def test_fast_matches_general_and_oracle(device, precision, out_dtype):
             label = "fast" if variant == "pairs" and shape[1] % 2 else variant  # odd heads: one per step
             assert _run(case, precision, variant) == [label], shape
         out_general = written(cases["general"])
-        for variant in ("sliced", "pairs", "fast"):
+        for variant in ("pairs", "fast"):
             assert np.array_equal(written(cases[variant]), out_general), f"{shape}: {variant} and general kernels differ"
-        _check_bound(cases["sliced"], precision)
+        _check_bound(cases["pairs"], precision)
         # Tokens outside the slot are untouched.
         layout, token_offset = shape[0], shape[6]
-        tensor = cases["sliced"].job.destination.tensor
+        tensor = cases["pairs"].job.destination.tensor
         canonical = (tensor.transpose(1, 2) if layout == "BHTD" else tensor).reshape(-1, shape[1] * shape[2])
         tokens = int(np.prod(shape[5]))
         assert bool((canonical[:token_offset] == -123.0).all())
@@ -112,11 +109,6 @@ def test_fast_pictures_and_mixed_groups(device):
     assert sorted(handle.stats["variants"]) == ["pairs", "pairs"]
     for case, want in zip(cases, paired):
         assert torch.equal(case.job.destination.slot(case.job.tokens), want)  # same bits, one launch per group
-    handle = rk.reconstruct([case.job for case in cases], config={"slice_variant": True})
-    handle.release()
-    assert sorted(handle.stats["variants"]) == ["pairs", "sliced"]
-    for case in cases:
-        _check_bound(case, "fp16x2")
 
 
 def test_unaligned_jobs_use_the_general_kernel(device):
