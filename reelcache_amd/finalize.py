@@ -196,9 +196,9 @@ def _rank_terms(coefficients, rows):
     return traces, info.double(), eta.double(), largest.double()
 
 
-def _measure_group(items, ranks):
-    """Device measurements of tiles sharing a channel count and dtype; one host transfer.
-    Returns (coefficients, per-item host scalar dicts)."""
+def _launch_group(items, ranks):
+    """Device measurements of tiles sharing a channel count and dtype, launched: (coefficients,
+    the device scalars that :func:`_read_group` transfers)."""
     sources = [item.matrix for item in items]
     rows = [item.rows16 for item in items]
     keys = fit_kernels.absmax(sources)
@@ -212,12 +212,38 @@ def _measure_group(items, ranks):
     for members in by_rank.values():
         values = _rank_terms([coefficients[i] for i in members], [rows[i] for i in members])
         terms[:, members] = torch.stack(values)
-    scalars = torch.cat((keys.double(), totals.reshape(-1), terms.reshape(-1), extrema.double().reshape(-1)))
+    return coefficients, torch.cat((keys.double(), totals.reshape(-1), terms.reshape(-1), extrema.double().reshape(-1)))
+
+
+def _read_group(launched):
+    """(coefficients, per-item host scalar dicts) of a :func:`_launch_group`; one host transfer."""
+    coefficients, scalars = launched
+    n = len(coefficients)
     scalars = scalars.cpu().numpy()
     fields = {"bits": scalars[:n], "totals": scalars[n:3 * n].reshape(n, 2), "traces": scalars[3 * n:4 * n],
               "info": scalars[4 * n:5 * n], "eta": scalars[5 * n:6 * n], "largest": scalars[6 * n:7 * n],
               "extrema": scalars[7 * n:].reshape(n, -1).astype(np.int64).astype(np.int32)}
     return coefficients, [{name: value[index] for name, value in fields.items()} for index in range(n)]
+
+
+class _Raised:
+    """An exception kept to be raised later."""
+
+    def __init__(self, error: BaseException):
+        self.error = error
+
+
+def _attempt(function, *args):
+    try:
+        return function(*args)
+    except Exception as error:  # raised again by _result, in the item's turn
+        return _Raised(error)
+
+
+def _result(value):
+    if isinstance(value, _Raised):
+        raise value.error
+    return value
 
 
 def _condition(eta: float, largest: float, rank: int, channels: int, rows16: torch.Tensor) -> float:
@@ -249,8 +275,19 @@ def finalize_tiles(items: Sequence[FinalizeItem], *, tile_rows: int, keep_coeffi
         groups.setdefault((int(item.matrix.shape[1]), item.matrix.dtype, item.matrix.device), []).append(index)
     coefficients: list = [None] * len(items)
     measured: list = [None] * len(items)
-    for members in groups.values():
-        values, scalars = _measure_group([items[i] for i in members], [ranks[i] for i in members])
+    launched = [(members, _launch_group([items[i] for i in members], [ranks[i] for i in members]))
+                for members in groups.values()]
+    # Host-only records of every item while the device measures: the picture layout and the
+    # stored rows as bytes (from the host copy when there is one).  An error raised here is
+    # raised again where the item's record is made, so errors keep the order of the items.
+    layouts: list = []
+    stored_rows: list = []
+    for item, rank in zip(items, ranks):
+        context, spec = item.context, item.spec
+        layouts.append(_attempt(video_layout, context.frames, context.height, context.width, rank, spec.pix_fmt))
+        stored_rows.append(None if item.host_rows is None else _attempt(rows_to_bytes, item.host_rows))
+    for members, pending in launched:
+        values, scalars = _read_group(pending)
         for position, index in enumerate(members):
             coefficients[index], measured[index] = values[position], scalars[position]
     _, _, finite = fit_kernels.split_keys_many(np.stack([m["extrema"] for m in measured]), ranks)
@@ -279,13 +316,13 @@ def finalize_tiles(items: Sequence[FinalizeItem], *, tile_rows: int, keep_coeffi
     for index, (item, rank, measures) in enumerate(zip(items, ranks, tiles)):
         pixels, affine, layout = codes[index]
         context, spec = item.context, item.spec
-        video = video_layout(context.frames, context.height, context.width, rank, spec.pix_fmt)
+        video = _result(layouts[index])
         gram = host_coefficients = None
         if keep_coefficients:
             rows64 = item.rows16.double()
             gram = (rows64 @ rows64.T).cpu().numpy()
             host_coefficients = coefficients[index].cpu().numpy()
-        basis = rows_to_bytes(item.rows16 if item.host_rows is None else item.host_rows)
+        basis = rows_to_bytes(item.rows16) if stored_rows[index] is None else _result(stored_rows[index])
         tile = FinalTile(item.entry, context, spec, video, layout, affine.astype("<f4", copy=False).tobytes(), basis,
                          rank, (0, 0), *measures[:2], measures[2], measures[3], measures[4], measures[5],
                          host_coefficients, gram)
