@@ -111,6 +111,34 @@ def test_projection_batch_of_ragged_ranks(device):
         assert (p.cpu().numpy() == expected).mean() >= 0.999
 
 
+def test_basis_layouts_read_in_place_or_repadded_give_the_same_values(device):
+    """A stored basis is read in place when its rows are unit-stride, 16-byte aligned and 16-byte
+    pitched, else through a zero-padded copy.  Row-major, column-major (a transposed view), a row
+    block at an odd element offset and a wider pitch must all give the same coefficients and
+    energies, bit for bit."""
+    rng = np.random.default_rng(41)
+    channels, rank = 128, 24
+    x, _ = _source(rng, 300, channels, "bfloat16", device, spectrum=True)
+    q, _ = _basis(rng, rank, channels, device)
+    column_major = q.T.contiguous().T                      # strides (1, rank)
+    wide = torch.zeros((rank, channels + 8), dtype=q.dtype, device=device)
+    wide[:, :channels] = q
+    pitched = wide[:, :channels]                            # row pitch 136 elements (272 bytes)
+    shifted_storage = torch.zeros(rank * channels + 1, dtype=q.dtype, device=device)
+    shifted = shifted_storage[1:].view(rank, channels)      # address 2 bytes past a 16-byte boundary
+    shifted.copy_(q)
+    layouts = [q, column_major, pitched, shifted]
+    assert column_major.stride() == (1, rank) and shifted.data_ptr() % 16 == 2
+    keys = fk.absmax([x] * len(layouts))
+    coefficients, extrema = fk.project([x] * len(layouts), layouts, [rank] * len(layouts), extrema=True)
+    totals = fk.energies([x] * len(layouts), keys, bases=layouts, ranks=[rank] * len(layouts),
+                         coefficients=coefficients).cpu().numpy()
+    for p, total, row in zip(coefficients[1:], totals[1:], extrema[1:]):
+        assert torch.equal(p, coefficients[0])
+        assert np.array_equal(total, totals[0])
+        assert torch.equal(row, extrema[0])
+
+
 @pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
 def test_energies_match_fp64(device, dtype):
     rng = np.random.default_rng(15)
