@@ -57,8 +57,10 @@ def _little_endian():
 
 
 def _finite_fp16(data) -> bool:
+    # A value is inf / nan when its exponent bits are all ones, i.e. when its magnitude bits are
+    # at least the exponent mask: one masked maximum decides for the whole block.
     bits = np.frombuffer(data, dtype=np.uint16)
-    return not bool(((bits & _EXPONENT_BITS) == _EXPONENT_BITS).any())
+    return bits.size == 0 or int((bits & np.uint16(0x7FFF)).max()) < int(_EXPONENT_BITS)
 
 
 def rows_to_bytes(rows: torch.Tensor) -> bytes:

@@ -363,26 +363,31 @@ def quantize_batched(values, affines) -> list[torch.Tensor]:
     device = _device(values)
     if len(values) != len(affines) or not values:
         raise ConfigurationError("batched quantization needs one affine per matrix")
-    parts, codes = [], []
-    table = np.zeros(len(values), dtype=_lib.QUANTIZE_DTYPE)
-    offsets = [0]
-    for v, affine in zip(values, affines):
-        affine = np.ascontiguousarray(affine, dtype=np.float64)
-        if (v.dtype != torch.float32 or v.ndim != 2 or min(v.shape) < 1 or v.stride(1) != 1
-                or affine.shape != (2, v.shape[1])):
+    shapes = [v.shape for v in values]
+    parts = []
+    for v, shape, affine in zip(values, shapes, affines):
+        affine = np.asarray(affine, dtype=np.float64)
+        if (v.dtype != torch.float32 or len(shape) != 2 or min(shape) < 1 or v.stride(1) != 1
+                or affine.shape != (2, shape[1])):
             raise ConfigurationError("batched quantization takes nonempty fp32 matrices and [2, cols] affines")
-        parts.append(affine.reshape(-1))
-        offsets.append(offsets[-1] + affine.size)
+        parts.append(affine.reshape(-1))  # a copy when the affine is a strided view
+    rows = [int(shape[0]) for shape in shapes]
+    cols = [int(shape[1]) for shape in shapes]
     host = torch.from_numpy(np.concatenate(parts))
     device_affine = host.to(device)
-    for index, v in enumerate(values):
-        out = torch.empty(v.shape, dtype=torch.uint8, device=device)
-        codes.append(out)
-        row = table[index]
-        row["values_ptr"], row["rows"], row["cols"], row["stride"] = v.data_ptr(), v.shape[0], v.shape[1], v.stride(0)
-        row["affine_ptr"] = device_affine.data_ptr() + 8 * offsets[index]
-        row["codes_ptr"], row["code_stride"] = out.data_ptr(), out.stride(0)
+    # Every matrix's codes in one allocation: matrix i's [rows, cols] block at element offset first_i.
+    sizes = [r * c for r, c in zip(rows, cols)]
+    firsts = np.concatenate(([0], np.cumsum(sizes[:-1], dtype=np.int64)))
+    storage = torch.empty(int(sum(sizes)), dtype=torch.uint8, device=device)
+    codes = [torch.as_strided(storage, (r, c), (c, 1), int(first)) for r, c, first in zip(rows, cols, firsts)]
+    table = np.zeros(len(values), dtype=_lib.QUANTIZE_DTYPE)
+    table["values_ptr"] = [v.data_ptr() for v in values]
+    table["rows"] = rows
+    table["cols"] = cols
+    table["stride"] = [v.stride(0) for v in values]
+    table["affine_ptr"] = device_affine.data_ptr() + 16 * np.concatenate(([0], np.cumsum(cols[:-1], dtype=np.int64)))
+    table["codes_ptr"] = storage.data_ptr() + firsts
+    table["code_stride"] = cols
     descriptors = _upload(table, device)
-    _lib.call("rch_quantize_batched", descriptors.data_ptr(), len(values), max(int(v.shape[0]) for v in values),
-              _stream(device))
+    _lib.call("rch_quantize_batched", descriptors.data_ptr(), len(values), max(rows), _stream(device))
     return codes

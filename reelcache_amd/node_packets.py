@@ -198,11 +198,14 @@ def quantize_many(coefficients, keys, specs):
     for p in coefficients:
         _check(p)
         ranks.append(int(p.shape[1]))
-    width = max((len(np.asarray(row)) for row in keys), default=0)
-    block = np.zeros((len(ranks), width), dtype=np.int64)
-    for index, row in enumerate(keys):
-        row = np.asarray(row)
-        block[index, :len(row)] = row
+    rows = [np.asarray(row) for row in keys]
+    width = max((len(row) for row in rows), default=0)
+    if rows and all(len(row) == width for row in rows):
+        block = np.stack(rows).astype(np.int64)  # rows of one key block (the common case)
+    else:
+        block = np.zeros((len(ranks), width), dtype=np.int64)
+        for index, row in enumerate(rows):
+            block[index, :len(row)] = row
     lows, highs, finite = fit_kernels.split_keys_many(block, ranks)
     if not all(finite):
         raise ConfigurationError("coefficients must be finite")
@@ -222,8 +225,11 @@ def quantize_many(coefficients, keys, specs):
             payloads[index] = np.ascontiguousarray(covered[:, position])
     affines, outputs, values = [], [], []
     for p, rank, layout, affine in zip(coefficients, ranks, layouts, payloads):
-        scale, offset = expanded_affine(affine, layout, rank)
-        affines.append(np.stack((np.asarray(scale, np.float64), np.asarray(offset, np.float64))))
+        if layout["mode"] == "per_channel":  # the payload is the per-column (scale; offset) itself
+            affines.append(affine.astype(np.float64))
+        else:
+            scale, offset = expanded_affine(affine, layout, rank)
+            affines.append(np.stack((np.asarray(scale, np.float64), np.asarray(offset, np.float64))))
         values.append(p if p.stride(1) == 1 else p.contiguous())
     layouts = [(affine.astype("<f4", copy=False), layout) for affine, layout in zip(payloads, layouts)]
     codes = fit_kernels.quantize_batched(values, affines)
