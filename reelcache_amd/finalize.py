@@ -211,7 +211,13 @@ def _launch_group(items, ranks):
         by_rank.setdefault(rank, []).append(index)
     for members in by_rank.values():
         values = _rank_terms([coefficients[i] for i in members], [rows[i] for i in members])
-        terms[:, members] = torch.stack(values)
+        # Consecutive members (one rank: the usual case) take a slice; others an index tensor
+        # copied from pinned memory without a host wait (a pageable copy would drain the stream).
+        if members == list(range(members[0], members[0] + len(members))):
+            index = slice(members[0], members[0] + len(members))
+        else:
+            index = torch.tensor(members, dtype=torch.long).pin_memory().to(terms.device, non_blocking=True)
+        terms[:, index] = torch.stack(values)
     return coefficients, torch.cat((keys.double(), totals.reshape(-1), terms.reshape(-1), extrema.double().reshape(-1)))
 
 
